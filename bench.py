@@ -1,0 +1,294 @@
+#!/usr/bin/env python3
+"""FP8 save + restore of Qwen3-8B-shaped KV blocks on one MI355X through libkvx.
+
+Workload: a [2, 36, 320, 256, 8, 128] bf16 pool holding 0.5 * t(df=4) values
+with 4 seeded outlier channels (x20) per (K/V, layer, KV head). One step saves
+128 seeded blocks (gather + per-(token, head) e4m3 quantisation, fp32 scales)
+into HBM-resident entries and restores those entries into 128 other seeded
+blocks (dequantisation + scatter): one launch each, inputs resident in HBM.
+
+`value` is logical KV throughput: BF16-equivalent bytes saved + restored per
+second (37,748,736 B per block and direction). `roofline` prices the
+dominant kernel's algorithmic HBM bytes (57,212,928 B per block: 36 MiB bf16
+read, 18 MiB e4m3 + 576 KiB fp32 scales written, or the reverse) per launch
+against 8 TB/s, timed with HIP events on its stream. `host_link` reports the
+same blocks moved to and from pinned host slabs through the copy engine
+(PCIe-inclusive; not `value`). `cpu_baseline` times the reference's CPU path
+(its torch codec on CPU tensors) on a bounded sample of the same blocks.
+
+Run: python bench.py [--steps 50] [--warmup 5] [--blocks 128]
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "kv-cache-offloading_amd"))
+sys.path.insert(0, str(ROOT))
+
+METRIC = "KV GB/s FP8 save+restore, Qwen3-8B blocks (% HBM & host-link roofline)"
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+PCIE_PEAK_GBS = 63.0        # PCIe 5.0 x16, per direction (raw 64 GT/s x16 after 128b/130b)
+BF16_BLOCK_BYTES = 37_748_736
+
+
+def log(*args):
+    print(*args, file=sys.stderr, flush=True)
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--blocks", type=int, default=128, help="blocks saved and restored per step")
+    p.add_argument("--scale", choices=("fp32", "bf16"), default="fp32")
+    p.add_argument("--skip-host-link", action="store_true")
+    p.add_argument("--skip-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample budget")
+    p.add_argument("--host-reps", type=int, default=3)
+    return p.parse_args()
+
+
+def kernel_leg(torch, ops, pool, sources, dests, scale_dtype, steps, warmup):
+    """HBM-resident save + restore; returns timings and algorithmic byte counts."""
+    layout = ops.pool_layout(pool, scale_dtype)
+    logical, offset, stride = ops.entry_layout(layout, ops.FORMAT_FP8)
+    n = len(sources)
+    staging = torch.empty(n * stride, dtype=torch.uint8, device=pool.device)
+    entries = [staging.data_ptr() + i * stride for i in range(n)]
+    stream = torch.cuda.current_stream(pool.device)
+
+    def step(events=None):
+        if events:
+            events[0].record(stream)
+        ops.save_blocks(pool, sources, entries, ops.FORMAT_FP8, scale_dtype)
+        if events:
+            events[1].record(stream)
+        ops.restore_blocks(pool, dests, entries, ops.FORMAT_FP8, scale_dtype)
+        if events:
+            events[2].record(stream)
+
+    for _ in range(warmup):
+        step()
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for ev in events:
+        step(ev)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    save_ms = sum(e[0].elapsed_time(e[1]) for e in events) / steps
+    restore_ms = sum(e[1].elapsed_time(e[2]) for e in events) / steps
+    hbm_bytes = n * (BF16_BLOCK_BYTES + logical)  # per launch, either direction
+    return dict(elapsed=elapsed, save_ms=save_ms, restore_ms=restore_ms, hbm_bytes=hbm_bytes,
+                logical_entry=logical, entry_stride=stride)
+
+
+def host_link_leg(torch, pool, layout, sources, dests, reps):
+    """Saves to / restores from pinned host slabs through the copy engine; D2H, H2D, both at once."""
+    from kvx import ops
+    from kvx.engine.cpu_prefix_cache import _CopyEngine
+
+    n = len(sources)
+    engine = _CopyEngine(pool, layout, ops.FORMAT_FP8, split=True)
+    try:
+        stride = engine.entry_stride
+        link_bytes = n * engine.logical_bytes
+        t = time.perf_counter()
+        slab = torch.empty(2 * n * stride, dtype=torch.uint8, pin_memory=True)
+        pin_s = time.perf_counter() - t
+        save_staging = torch.empty(n * stride, dtype=torch.uint8, device=pool.device)
+        restore_staging = torch.empty(n * stride, dtype=torch.uint8, device=pool.device)
+        engine.add_slab(slab, 2 * n)
+        engine.set_staging(save_staging, restore_staging, n)
+        compute = torch.cuda.current_stream(pool.device).cuda_stream
+        low, high = list(range(n)), list(range(n, 2 * n))
+
+        def timed(fn):
+            best = None
+            for _ in range(reps):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                fn()
+                engine.synchronize()
+                torch.cuda.synchronize()
+                dt = time.perf_counter() - t0
+                best = dt if best is None else min(best, dt)
+            return best
+
+        engine.save(sources, low, compute)  # fill the restore source slots
+        engine.synchronize()
+        save_s = timed(lambda: engine.save(sources, high, compute))
+        restore_s = timed(lambda: engine.restore(low, dests, False, compute))
+
+        def both():
+            engine.save(sources, high, compute)
+            engine.restore(low, dests, False, compute)
+
+        both_s = timed(both)
+
+        # Ceiling: one contiguous pinned copy each way, and both at once on two streams.
+        flat_dev = torch.empty(link_bytes, dtype=torch.uint8, device=pool.device)
+        flat_host = slab[:link_bytes]
+        flat_host2 = slab[n * stride:n * stride + link_bytes]
+        s1, s2 = torch.cuda.Stream(pool.device), torch.cuda.Stream(pool.device)
+
+        def d2h():
+            with torch.cuda.stream(s1):
+                flat_host.copy_(flat_dev, non_blocking=True)
+
+        def h2d():
+            with torch.cuda.stream(s2):
+                flat_dev2.copy_(flat_host2, non_blocking=True)
+
+        flat_dev2 = torch.empty_like(flat_dev)
+        ceil_d2h = timed(d2h)
+        ceil_h2d = timed(h2d)
+        ceil_both = timed(lambda: (d2h(), h2d()))
+        gbs = lambda nbytes, s: nbytes / s / 1e9  # noqa: E731
+        overlap = (save_s + restore_s - both_s) / min(save_s, restore_s)
+        duplex = gbs(2 * link_bytes, both_s)
+        return {
+            "bytes_per_direction": link_bytes,
+            "save_d2h_gbs": round(gbs(link_bytes, save_s), 2),
+            "restore_h2d_gbs": round(gbs(link_bytes, restore_s), 2),
+            "duplex_gbs": round(duplex, 2),
+            "overlap_fraction": round(overlap, 3),
+            "ceiling_memcpy_d2h_gbs": round(gbs(link_bytes, ceil_d2h), 2),
+            "ceiling_memcpy_h2d_gbs": round(gbs(link_bytes, ceil_h2d), 2),
+            "ceiling_memcpy_duplex_gbs": round(gbs(2 * link_bytes, ceil_both), 2),
+            "peak_per_direction_gbs": PCIE_PEAK_GBS,
+            "frac_duplex_of_spec": round(duplex / (2 * PCIE_PEAK_GBS), 3),
+            "frac_duplex_of_measured_ceiling": round(duplex / gbs(2 * link_bytes, ceil_both), 3),
+            "pin_seconds": round(pin_s, 2),
+            "logical_kv_gbs": round(2 * n * BF16_BLOCK_BYTES / both_s / 1e9, 2),
+        }
+    finally:
+        engine.close()
+
+
+def cpu_baseline_leg(torch, shape, scale_dtype, seconds):
+    """The reference's CPU path (its torch codec on CPU tensors) on Qwen3-8B blocks."""
+    from oracle import torch_path
+
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    torch.set_num_threads(threads)
+    cpu_blocks = 4
+    g = torch.Generator().manual_seed(0)
+    pool = (torch.randn((2, shape[1], cpu_blocks, *shape[3:]), generator=g) * 0.5).to(torch.bfloat16)
+    block_shape = (2, shape[1], *shape[3:])
+    payload = torch.empty(block_shape, dtype=torch.float8_e4m3fn)
+    scale = torch.empty((*block_shape[:-1], 1), dtype=scale_dtype)
+    torch_path.save_block(pool, 0, payload, scale)  # warm-up
+    moved, t0 = 0, time.perf_counter()
+    while True:
+        b = moved // 2 % cpu_blocks
+        torch_path.save_block(pool, b, payload, scale)
+        torch_path.restore_block(pool, (b + 1) % cpu_blocks, payload, scale)
+        moved += 2
+        elapsed = time.perf_counter() - t0
+        if elapsed >= seconds:
+            break
+    return {
+        "value": round(moved * BF16_BLOCK_BYTES / elapsed / 1e9, 3),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{moved // 2} save+restore pairs of Qwen3-8B blocks (FP8, {str(scale_dtype)[6:]} scales) "
+                  f"through torch's CPU codec (cpu_prefix_cache.py:20-28, 323-326, 394-397), {elapsed:.1f} s",
+    }
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: the KV copy path is per GPU and this build runs on a single "
+              f"MI355X (asked for --gpus {args.gpus}, WORLD_SIZE {world})", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from kvx import ops
+    from kvx.workloads import QWEN3_8B, block_selection, fill_student_t
+
+    if not torch.cuda.is_available():
+        sys.exit("bench.py needs a ROCm GPU")
+    device = torch.device("cuda", 0)
+    scale_dtype = torch.float32 if args.scale == "fp32" else torch.bfloat16
+    shape = QWEN3_8B.shape
+    log(f"pool {shape} bf16 on {torch.cuda.get_device_name(device)}")
+    pool = torch.empty(shape, dtype=torch.bfloat16, device=device)
+    fill_student_t(pool, seed=0)
+    torch.cuda.synchronize()
+    order = block_selection(QWEN3_8B.num_blocks, 2 * args.blocks, seed=1)
+    sources, dests = order[:args.blocks], order[args.blocks:]
+
+    k = kernel_leg(torch, ops, pool, sources, dests, scale_dtype, args.steps, args.warmup)
+    ms_per_step = 1000 * k["elapsed"] / args.steps
+    value = 2 * args.blocks * BF16_BLOCK_BYTES / (ms_per_step / 1000) / 1e9
+    save_gbs = k["hbm_bytes"] / (k["save_ms"] / 1000) / 1e9
+    restore_gbs = k["hbm_bytes"] / (k["restore_ms"] / 1000) / 1e9
+    dominant = "save" if k["save_ms"] >= k["restore_ms"] else "restore"
+    achieved = min(save_gbs, restore_gbs)
+    log(f"step {ms_per_step:.3f} ms; save {k['save_ms']:.3f} ms ({save_gbs:.0f} GB/s), "
+        f"restore {k['restore_ms']:.3f} ms ({restore_gbs:.0f} GB/s)")
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "qwen3-8b-kv-fp8-save-restore",
+            "pool": list(shape),
+            "blocks_saved": args.blocks,
+            "blocks_restored": args.blocks,
+            "scale_dtype": args.scale,
+            "storage": "bf16 pool -> e4m3fn payload + per-(token, kv-head) scale",
+            "values": "bf16 0.5*t(df=4), 4 outlier channels x20 per (kv, layer, head)",
+            "residency": "pool and entries in HBM",
+        },
+        "blocks_per_s": round(2 * args.blocks / (ms_per_step / 1000), 1),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": f"fp8_{dominant}_kernel",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+        "kernels": {
+            "save": {"ms": round(k["save_ms"], 4), "hbm_gbs": round(save_gbs, 1),
+                     "frac": round(save_gbs / HBM_PEAK_GBS, 4)},
+            "restore": {"ms": round(k["restore_ms"], 4), "hbm_gbs": round(restore_gbs, 1),
+                        "frac": round(restore_gbs / HBM_PEAK_GBS, 4)},
+            "algorithmic_bytes_per_launch": k["hbm_bytes"],
+        },
+    }
+    if not args.skip_host_link:
+        log("host link leg")
+        result["host_link"] = host_link_leg(torch, pool, ops.pool_layout(pool, scale_dtype), sources, dests,
+                                            args.host_reps)
+    if not args.skip_cpu_baseline:
+        log("cpu baseline leg")
+        result["cpu_baseline"] = cpu_baseline_leg(torch, shape, scale_dtype, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,561 @@
+// C ABI of libkvx: argument checking, batching, and the copy engine that
+// orders saves and restores against the caller's compute stream.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <new>
+#include <vector>
+
+#include "kvx_internal.h"
+
+namespace kvx {
+
+static thread_local char g_error[512] = "";
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_status(hipError_t err, const char* what) {
+  if (err == hipSuccess) return KVX_OK;
+  return set_error((int)err, "%s: %s (hipError_t %d)", what, hipGetErrorString(err), (int)err);
+}
+
+int check_layout(const kvx_block_layout* l, int32_t format) {
+  if (!l) return set_error(KVX_E_INVALID, "layout is NULL");
+  if (format != KVX_FORMAT_RAW && format != KVX_FORMAT_FP8)
+    return set_error(KVX_E_INVALID, "unknown entry format %d", format);
+  if (l->planes <= 0 || l->plane_rows <= 0 || l->head_dim <= 0 || l->num_blocks <= 0)
+    return set_error(KVX_E_INVALID, "layout sizes must be positive (planes %d, rows %d, head_dim %d, blocks %d)",
+                     l->planes, l->plane_rows, l->head_dim, l->num_blocks);
+  if (l->plane_stride < 0 || l->block_stride < 0)
+    return set_error(KVX_E_INVALID, "layout strides must be non-negative");
+  const int64_t plane_elems = (int64_t)l->plane_rows * l->head_dim;
+  if (l->num_blocks > 1 && l->block_stride < plane_elems)
+    return set_error(KVX_E_INVALID, "block_stride %lld overlaps a %lld-element plane",
+                     (long long)l->block_stride, (long long)plane_elems);
+  if (format == KVX_FORMAT_FP8) {
+    if (l->elem_bytes != 2) return set_error(KVX_E_UNSUPPORTED, "FP8 entries need bf16 (2-byte) pool elements");
+    if (l->scale_dtype != KVX_SCALE_BF16 && l->scale_dtype != KVX_SCALE_FP32)
+      return set_error(KVX_E_INVALID, "unknown scale dtype %d", l->scale_dtype);
+  } else if (l->elem_bytes != 1 && l->elem_bytes != 2 && l->elem_bytes != 4 && l->elem_bytes != 8) {
+    return set_error(KVX_E_INVALID, "elem_bytes must be 1, 2, 4 or 8");
+  }
+  // Launch grids: blocks * planes * tiles must fit a 32-bit workgroup count.
+  if ((int64_t)kMaxBatch * l->planes * ((plane_elems * l->elem_bytes) / 16 + 1) > (int64_t)INT32_MAX)
+    return set_error(KVX_E_UNSUPPORTED, "block geometry too large for one launch");
+  return KVX_OK;
+}
+
+static void entry_sizes(const kvx_block_layout& l, int32_t format, int64_t* logical, int64_t* scale_off,
+                        int64_t* stride) {
+  const int64_t rows = (int64_t)l.planes * l.plane_rows;
+  int64_t payload, bytes;
+  if (format == KVX_FORMAT_FP8) {
+    payload = rows * l.head_dim;
+    const int64_t sb = l.scale_dtype == KVX_SCALE_BF16 ? 2 : 4;
+    // The reference budgets payload + scales (cpu_prefix_cache.py:98-100).
+    *logical = payload + rows * sb;
+    *scale_off = (payload + 255) / 256 * 256;
+    bytes = *scale_off + rows * sb;
+  } else {
+    payload = rows * l.head_dim * l.elem_bytes;
+    *logical = payload;
+    *scale_off = 0;
+    bytes = payload;
+  }
+  *stride = (bytes + 255) / 256 * 256;
+}
+
+// Splits (ids, entries) into launches of at most kMaxBatch blocks.
+static int run_batches(bool save, void* pool, const kvx_block_layout* layout, int32_t format,
+                       const int32_t* ids, const uint64_t* entries, int32_t n, int64_t scale_offset,
+                       hipStream_t stream) {
+  int rc = check_layout(layout, format);
+  if (rc) return rc;
+  if (n < 0) return set_error(KVX_E_INVALID, "negative block count");
+  if (n == 0) return KVX_OK;
+  if (!pool || !ids || !entries) return set_error(KVX_E_INVALID, "NULL pool, block id or entry array");
+  const int64_t sbytes = layout->scale_dtype == KVX_SCALE_BF16 ? 2 : 4;
+  const bool vec_pool = layout->head_dim % 8 == 0;
+  for (int32_t i = 0; i < n; ++i) {
+    if (ids[i] < 0 || ids[i] >= layout->num_blocks)
+      return set_error(KVX_E_RANGE, "block id %d outside [0, %d)", ids[i], layout->num_blocks);
+    if (!entries[i]) return set_error(KVX_E_INVALID, "entry %d is NULL", i);
+    const uint64_t align = format == KVX_FORMAT_FP8 ? (vec_pool ? 8 : 1) : 2;
+    if (entries[i] % align) return set_error(KVX_E_INVALID, "entry %d is not %llu-byte aligned", i,
+                                             (unsigned long long)align);
+    if (format == KVX_FORMAT_FP8 && (entries[i] + (uint64_t)scale_offset) % (uint64_t)sbytes)
+      return set_error(KVX_E_INVALID, "scales of entry %d are misaligned", i);
+  }
+  if ((uintptr_t)pool % 2) return set_error(KVX_E_INVALID, "pool is not 2-byte aligned");
+  BlockBatch b;
+  for (int32_t base = 0; base < n; base += kMaxBatch) {
+    b.n = std::min(kMaxBatch, n - base);
+    for (int32_t i = 0; i < b.n; ++i) {
+      b.ids[i] = ids[base + i];
+      b.entries[i] = entries[base + i];
+    }
+    const bool vec = vector_access_ok(pool, *layout, b.entries, b.n);
+    hipError_t err = save ? launch_save(pool, *layout, format, b, scale_offset, vec, stream)
+                          : launch_restore(pool, *layout, format, b, scale_offset, vec, stream);
+    if (err != hipSuccess) return hip_status(err, save ? "save kernel launch" : "restore kernel launch");
+  }
+  return KVX_OK;
+}
+
+}  // namespace kvx
+
+using namespace kvx;
+
+// ---------------------------------------------------------------------------
+// Copy engine
+
+namespace {
+
+struct Event {
+  hipEvent_t ev = nullptr;
+  int refs = 0;
+};
+
+struct Slab {
+  uint8_t* base;
+  int32_t first;
+  int32_t count;
+};
+
+}  // namespace
+
+struct kvx_cache {
+  int device = 0;
+  uint8_t* pool = nullptr;
+  kvx_block_layout layout{};
+  int32_t format = KVX_FORMAT_RAW;
+  int64_t logical_bytes = 0, scale_offset = 0, entry_stride = 0;
+  bool split = false;
+  hipStream_t save_stream = nullptr, restore_stream = nullptr;
+  hipEvent_t marker = nullptr;  // makes one stream wait for everything queued on another
+  uint8_t* save_staging = nullptr;
+  uint8_t* restore_staging = nullptr;
+  int32_t staging_entries = 0;
+  std::vector<Slab> slabs;
+  int32_t num_slots = 0;
+  std::vector<Event*> pending_save, pending_restore;  // per GPU block
+  std::vector<Event*> slot_read, slot_saved;          // per host slot
+  std::vector<Event*> free_events, all_events;
+  int64_t saved = 0, restored = 0, waits = 0;
+
+  uint8_t* host_entry(int32_t slot) const {
+    for (const Slab& s : slabs)
+      if (slot >= s.first && slot < s.first + s.count) return s.base + (int64_t)(slot - s.first) * entry_stride;
+    return nullptr;
+  }
+
+  int new_event(Event** out) {
+    Event* e;
+    if (!free_events.empty()) {
+      e = free_events.back();
+      free_events.pop_back();
+    } else {
+      e = new (std::nothrow) Event();
+      if (!e) return set_error(KVX_E_STATE, "out of host memory for events");
+      hipError_t err = hipEventCreateWithFlags(&e->ev, hipEventDisableTiming);
+      if (err != hipSuccess) {
+        delete e;
+        return hip_status(err, "hipEventCreateWithFlags");
+      }
+      all_events.push_back(e);
+    }
+    e->refs = 0;
+    *out = e;
+    return KVX_OK;
+  }
+
+  void unref(Event*& e) {
+    if (!e) return;
+    if (--e->refs == 0) free_events.push_back(e);
+    e = nullptr;
+  }
+
+  void assign(Event*& slot, Event* e) {
+    unref(slot);
+    ++e->refs;
+    slot = e;
+  }
+
+  void release_if_unused(Event* e) {
+    if (e->refs == 0) free_events.push_back(e);
+  }
+
+  int wait_event(hipStream_t s, Event* e) {
+    ++waits;
+    return hip_status(hipStreamWaitEvent(s, e->ev, 0), "hipStreamWaitEvent");
+  }
+
+  // `dst` waits for all work queued so far on `src`.
+  int wait_stream(hipStream_t dst, hipStream_t src) {
+    if (dst == src) return KVX_OK;
+    int rc = hip_status(hipEventRecord(marker, src), "hipEventRecord");
+    if (rc) return rc;
+    ++waits;
+    return hip_status(hipStreamWaitEvent(dst, marker, 0), "hipStreamWaitEvent");
+  }
+
+  int check_lists(const int32_t* ids, const int32_t* slots, int32_t n) const {
+    if (n < 0) return set_error(KVX_E_INVALID, "negative block count");
+    if (n > 0 && (!ids || !slots)) return set_error(KVX_E_INVALID, "NULL block id or slot array");
+    for (int32_t i = 0; i < n; ++i) {
+      if (ids[i] < 0 || ids[i] >= layout.num_blocks)
+        return set_error(KVX_E_RANGE, "block id %d outside [0, %d)", ids[i], layout.num_blocks);
+      if (slots[i] < 0 || slots[i] >= num_slots)
+        return set_error(KVX_E_RANGE, "host slot %d outside [0, %d)", slots[i], num_slots);
+    }
+    if (n > 0 && !save_staging) return set_error(KVX_E_STATE, "no staging attached");
+    return KVX_OK;
+  }
+
+  // Copies `count` entries between consecutive staging entries and host
+  // slots, merging runs of consecutive slots in one slab into one DMA.
+  int dma(bool to_host, uint8_t* staging, const int32_t* slots, int32_t count, hipStream_t s) {
+    int32_t i = 0;
+    while (i < count) {
+      int32_t j = i + 1;
+      uint8_t* h0 = host_entry(slots[i]);
+      while (j < count && slots[j] == slots[j - 1] + 1 && host_entry(slots[j]) == h0 + (int64_t)(j - i) * entry_stride)
+        ++j;
+      const size_t bytes = (size_t)(j - i - 1) * entry_stride + (size_t)logical_bytes_with_scales();
+      uint8_t* d = staging + (int64_t)i * entry_stride;
+      hipError_t err = to_host ? hipMemcpyAsync(h0, d, bytes, hipMemcpyDeviceToHost, s)
+                               : hipMemcpyAsync(d, h0, bytes, hipMemcpyHostToDevice, s);
+      if (err != hipSuccess) return hip_status(err, to_host ? "D2H hipMemcpyAsync" : "H2D hipMemcpyAsync");
+      i = j;
+    }
+    return KVX_OK;
+  }
+
+  // Bytes of one entry that carry data (payload, and scales at scale_offset).
+  int64_t logical_bytes_with_scales() const {
+    if (format == KVX_FORMAT_RAW) return logical_bytes;
+    const int64_t rows = (int64_t)layout.planes * layout.plane_rows;
+    return scale_offset + rows * (layout.scale_dtype == KVX_SCALE_BF16 ? 2 : 4);
+  }
+
+  int launch(bool save, const int32_t* ids, uint8_t* staging, int32_t count, hipStream_t s) {
+    BlockBatch b;
+    b.n = count;
+    for (int32_t i = 0; i < count; ++i) {
+      b.ids[i] = ids[i];
+      b.entries[i] = (uint64_t)(uintptr_t)(staging + (int64_t)i * entry_stride);
+    }
+    const bool vec = vector_access_ok(pool, layout, b.entries, b.n);
+    hipError_t err = save ? launch_save(pool, layout, format, b, scale_offset, vec, s)
+                          : launch_restore(pool, layout, format, b, scale_offset, vec, s);
+    return hip_status(err, save ? "save kernel launch" : "restore kernel launch");
+  }
+
+  int chunk() const { return std::min(staging_entries, kMaxBatch); }
+};
+
+extern "C" {
+
+const char* kvx_last_error(void) { return g_error; }
+
+int kvx_abi_version(void) { return KVX_ABI_VERSION; }
+
+int kvx_entry_layout(const kvx_block_layout* layout, int32_t format, int64_t* logical_bytes,
+                     int64_t* scale_offset, int64_t* entry_stride) {
+  int rc = check_layout(layout, format);
+  if (rc) return rc;
+  int64_t a, b, c;
+  entry_sizes(*layout, format, &a, &b, &c);
+  if (logical_bytes) *logical_bytes = a;
+  if (scale_offset) *scale_offset = b;
+  if (entry_stride) *entry_stride = c;
+  return KVX_OK;
+}
+
+int kvx_store_kvcache(const void* key, int64_t key_stride, const void* value, int64_t value_stride, void* k_cache,
+                      void* v_cache, const int32_t* slot_mapping, int64_t num_tokens, int32_t num_heads,
+                      int32_t head_dim, int32_t elem_bytes, int64_t cache_slots, void* stream) {
+  if (num_tokens < 0) return set_error(KVX_E_INVALID, "negative token count");
+  if (num_heads <= 0 || head_dim <= 0) return set_error(KVX_E_INVALID, "num_heads and head_dim must be positive");
+  if (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4 && elem_bytes != 8)
+    return set_error(KVX_E_INVALID, "elem_bytes must be 1, 2, 4 or 8");
+  if (key_stride < 0 || value_stride < 0 || cache_slots < 0)
+    return set_error(KVX_E_INVALID, "strides and cache_slots must be non-negative");
+  if (num_tokens == 0 || cache_slots == 0) return KVX_OK;
+  if (!key || !value || !k_cache || !v_cache || !slot_mapping)
+    return set_error(KVX_E_INVALID, "NULL tensor pointer");
+  if (num_tokens > (int64_t)INT32_MAX) return set_error(KVX_E_UNSUPPORTED, "too many tokens for one launch");
+  const int64_t row = (int64_t)num_heads * head_dim;
+  hipError_t err = launch_store_kvcache(key, key_stride, value, value_stride, k_cache, v_cache, slot_mapping,
+                                        num_tokens, row, elem_bytes, cache_slots, (hipStream_t)stream);
+  return hip_status(err, "store_kvcache launch");
+}
+
+int kvx_save_blocks(const void* pool, const kvx_block_layout* layout, int32_t format, const int32_t* block_ids_host,
+                    const uint64_t* entries_host, int32_t n, int64_t scale_offset, void* stream) {
+  return run_batches(true, const_cast<void*>(pool), layout, format, block_ids_host, entries_host, n, scale_offset,
+                     (hipStream_t)stream);
+}
+
+int kvx_restore_blocks(void* pool, const kvx_block_layout* layout, int32_t format, const int32_t* block_ids_host,
+                       const uint64_t* entries_host, int32_t n, int64_t scale_offset, void* stream) {
+  return run_batches(false, pool, layout, format, block_ids_host, entries_host, n, scale_offset,
+                     (hipStream_t)stream);
+}
+
+int kvx_sleep(void* stream, int64_t microseconds) {
+  if (microseconds < 0 || microseconds > 60LL * 1000 * 1000)
+    return set_error(KVX_E_RANGE, "sleep must be within [0, 60 s]");
+  return hip_status(launch_sleep((hipStream_t)stream, microseconds), "sleep kernel launch");
+}
+
+int kvx_selftest(uint64_t* counters, void* stream) {
+  if (!counters) return set_error(KVX_E_INVALID, "NULL counter array");
+  return hip_status(launch_selftest(counters, (hipStream_t)stream), "selftest launch");
+}
+
+int kvx_cache_create(void* pool, const kvx_block_layout* layout, int32_t format, int32_t split_streams,
+                     int32_t device, kvx_cache** out) {
+  if (!out) return set_error(KVX_E_INVALID, "NULL output handle");
+  *out = nullptr;
+  int rc = check_layout(layout, format);
+  if (rc) return rc;
+  if (!pool || (uintptr_t)pool % 16) return set_error(KVX_E_INVALID, "pool must be a 16-byte aligned pointer");
+  kvx_cache* c = new (std::nothrow) kvx_cache();
+  if (!c) return set_error(KVX_E_STATE, "out of host memory");
+  c->device = device;
+  c->pool = (uint8_t*)pool;
+  c->layout = *layout;
+  c->format = format;
+  entry_sizes(*layout, format, &c->logical_bytes, &c->scale_offset, &c->entry_stride);
+  c->split = split_streams != 0;
+  c->pending_save.assign(layout->num_blocks, nullptr);
+  c->pending_restore.assign(layout->num_blocks, nullptr);
+  rc = hip_status(hipSetDevice(device), "hipSetDevice");
+  if (!rc) rc = hip_status(hipStreamCreateWithFlags(&c->save_stream, hipStreamNonBlocking), "hipStreamCreate");
+  if (!rc && c->split)
+    rc = hip_status(hipStreamCreateWithFlags(&c->restore_stream, hipStreamNonBlocking), "hipStreamCreate");
+  if (!rc && !c->split) c->restore_stream = c->save_stream;
+  if (!rc) rc = hip_status(hipEventCreateWithFlags(&c->marker, hipEventDisableTiming), "hipEventCreate");
+  if (rc) {
+    kvx_cache_destroy(c);
+    return rc;
+  }
+  *out = c;
+  return KVX_OK;
+}
+
+int kvx_cache_destroy(kvx_cache* c) {
+  if (!c) return KVX_OK;
+  int rc = KVX_OK;
+  (void)hipSetDevice(c->device);
+  if (c->save_stream) rc = hip_status(hipStreamSynchronize(c->save_stream), "hipStreamSynchronize");
+  if (c->split && c->restore_stream) {
+    int rc2 = hip_status(hipStreamSynchronize(c->restore_stream), "hipStreamSynchronize");
+    if (!rc) rc = rc2;
+  }
+  for (Event* e : c->all_events) {
+    (void)hipEventDestroy(e->ev);
+    delete e;
+  }
+  if (c->marker) (void)hipEventDestroy(c->marker);
+  if (c->split && c->restore_stream) (void)hipStreamDestroy(c->restore_stream);
+  if (c->save_stream) (void)hipStreamDestroy(c->save_stream);
+  delete c;
+  return rc;
+}
+
+int kvx_cache_set_staging(kvx_cache* c, void* save_staging, void* restore_staging, int32_t entries) {
+  if (!c) return set_error(KVX_E_INVALID, "NULL cache");
+  if (entries <= 0 || !save_staging || !restore_staging)
+    return set_error(KVX_E_INVALID, "staging needs two buffers and a positive entry count");
+  if ((uintptr_t)save_staging % 256 || (uintptr_t)restore_staging % 256)
+    return set_error(KVX_E_INVALID, "staging buffers must be 256-byte aligned");
+  if (!c->split && save_staging != restore_staging)
+    return set_error(KVX_E_INVALID, "one stream shares one staging buffer");
+  c->save_staging = (uint8_t*)save_staging;
+  c->restore_staging = (uint8_t*)restore_staging;
+  c->staging_entries = entries;
+  return KVX_OK;
+}
+
+int kvx_cache_add_slab(kvx_cache* c, void* host_base, int32_t count) {
+  if (!c) return set_error(KVX_E_INVALID, "NULL cache");
+  if (!host_base || count <= 0) return set_error(KVX_E_INVALID, "slab needs memory and a positive slot count");
+  if ((uintptr_t)host_base % 256) return set_error(KVX_E_INVALID, "slab must be 256-byte aligned");
+  if ((int64_t)c->num_slots + count > (int64_t)INT32_MAX) return set_error(KVX_E_RANGE, "too many slots");
+  c->slabs.push_back(Slab{(uint8_t*)host_base, c->num_slots, count});
+  c->num_slots += count;
+  c->slot_read.resize(c->num_slots, nullptr);
+  c->slot_saved.resize(c->num_slots, nullptr);
+  return KVX_OK;
+}
+
+int kvx_cache_reset_slabs(kvx_cache* c) {
+  if (!c) return set_error(KVX_E_INVALID, "NULL cache");
+  int rc = kvx_cache_synchronize(c);
+  if (rc) return rc;
+  for (Event*& e : c->slot_read) c->unref(e);
+  for (Event*& e : c->slot_saved) c->unref(e);
+  c->slot_read.clear();
+  c->slot_saved.clear();
+  c->slabs.clear();
+  c->num_slots = 0;
+  return KVX_OK;
+}
+
+int kvx_cache_streams(kvx_cache* c, void** save_stream, void** restore_stream) {
+  if (!c) return set_error(KVX_E_INVALID, "NULL cache");
+  if (save_stream) *save_stream = (void*)c->save_stream;
+  if (restore_stream) *restore_stream = (void*)c->restore_stream;
+  return KVX_OK;
+}
+
+int kvx_cache_save(kvx_cache* c, const int32_t* ids, const int32_t* slots, int32_t n, void* compute_stream) {
+  if (!c) return set_error(KVX_E_INVALID, "NULL cache");
+  int rc = c->check_lists(ids, slots, n);
+  if (rc || n == 0) return rc;
+  rc = hip_status(hipSetDevice(c->device), "hipSetDevice");
+  if (rc) return rc;
+  hipStream_t s = c->save_stream;
+  // Start after the kernels that wrote these blocks (cpu_prefix_cache.py:310-311).
+  rc = c->wait_stream(s, (hipStream_t)compute_stream);
+  if (rc) return rc;
+  // With split streams, after the last restore that read each target slot (:312-314).
+  if (c->split) {
+    for (int32_t i = 0; i < n; ++i) {
+      Event*& r = c->slot_read[slots[i]];
+      if (r) {
+        rc = c->wait_event(s, r);
+        if (rc) return rc;
+        c->unref(r);
+      }
+    }
+  }
+  const int32_t step = c->chunk();
+  for (int32_t base = 0; base < n; base += step) {
+    const int32_t cnt = std::min(step, n - base);
+    rc = c->launch(true, ids + base, c->save_staging, cnt, s);
+    if (!rc) rc = c->dma(true, c->save_staging, slots + base, cnt, s);
+    if (rc) return rc;
+  }
+  Event* done = nullptr;
+  rc = c->new_event(&done);
+  if (!rc) rc = hip_status(hipEventRecord(done->ev, s), "hipEventRecord");
+  if (rc) {
+    if (done) c->release_if_unused(done);
+    return rc;
+  }
+  for (int32_t i = 0; i < n; ++i) {
+    c->assign(c->pending_save[ids[i]], done);
+    c->assign(c->slot_saved[slots[i]], done);
+  }
+  c->saved += n;
+  return KVX_OK;
+}
+
+int kvx_cache_restore(kvx_cache* c, const int32_t* slots, const int32_t* ids, int32_t n, int32_t wait,
+                      void* compute_stream) {
+  if (!c) return set_error(KVX_E_INVALID, "NULL cache");
+  int rc = c->check_lists(ids, slots, n);
+  if (rc || n == 0) return rc;
+  rc = hip_status(hipSetDevice(c->device), "hipSetDevice");
+  if (rc) return rc;
+  hipStream_t s = c->restore_stream;
+  hipStream_t compute = (hipStream_t)compute_stream;
+  // The destination may still be read by queued kernels (cpu_prefix_cache.py:375-379).
+  rc = c->wait_stream(s, compute);
+  if (rc) return rc;
+  if (c->split) {
+    for (int32_t i = 0; i < n; ++i) {
+      // The payload may still be arriving from its own save (:380-381).
+      Event* sv = c->slot_saved[slots[i]];
+      if (sv) {
+        rc = c->wait_event(s, sv);
+        if (rc) return rc;
+      }
+      // A save of the destination's previous contents may still be reading it.
+      Event* ps = c->pending_save[ids[i]];
+      if (ps && ps != sv) {
+        rc = c->wait_event(s, ps);
+        if (rc) return rc;
+      }
+    }
+  }
+  const int32_t step = c->chunk();
+  for (int32_t base = 0; base < n; base += step) {
+    const int32_t cnt = std::min(step, n - base);
+    rc = c->dma(false, c->restore_staging, slots + base, cnt, s);
+    if (!rc) rc = c->launch(false, ids + base, c->restore_staging, cnt, s);
+    if (rc) return rc;
+  }
+  Event* done = nullptr;
+  rc = c->new_event(&done);
+  if (!rc) rc = hip_status(hipEventRecord(done->ev, s), "hipEventRecord");
+  if (!rc && wait) rc = c->wait_event(compute, done);
+  if (rc) {
+    if (done) c->release_if_unused(done);
+    return rc;
+  }
+  for (int32_t i = 0; i < n; ++i) {
+    c->assign(c->slot_read[slots[i]], done);
+    if (!wait) c->assign(c->pending_restore[ids[i]], done);
+  }
+  c->release_if_unused(done);
+  c->restored += n;
+  return KVX_OK;
+}
+
+int kvx_cache_before_block_reuse(kvx_cache* c, int32_t block_id, void* compute_stream) {
+  if (!c) return set_error(KVX_E_INVALID, "NULL cache");
+  if (block_id < 0 || block_id >= c->layout.num_blocks)
+    return set_error(KVX_E_RANGE, "block id %d outside [0, %d)", block_id, c->layout.num_blocks);
+  for (std::vector<Event*>* pending : {&c->pending_save, &c->pending_restore}) {
+    Event*& e = (*pending)[block_id];
+    if (e) {
+      int rc = c->wait_event((hipStream_t)compute_stream, e);
+      if (rc) return rc;
+      c->unref(e);
+    }
+  }
+  return KVX_OK;
+}
+
+int kvx_cache_before_block_use(kvx_cache* c, int32_t block_id, void* compute_stream) {
+  if (!c) return set_error(KVX_E_INVALID, "NULL cache");
+  if (block_id < 0 || block_id >= c->layout.num_blocks)
+    return set_error(KVX_E_RANGE, "block id %d outside [0, %d)", block_id, c->layout.num_blocks);
+  Event*& e = c->pending_restore[block_id];
+  if (e) {
+    int rc = c->wait_event((hipStream_t)compute_stream, e);
+    if (rc) return rc;
+    c->unref(e);
+  }
+  return KVX_OK;
+}
+
+int kvx_cache_synchronize(kvx_cache* c) {
+  if (!c) return set_error(KVX_E_INVALID, "NULL cache");
+  int rc = hip_status(hipSetDevice(c->device), "hipSetDevice");
+  if (!rc) rc = hip_status(hipStreamSynchronize(c->save_stream), "hipStreamSynchronize");
+  if (!rc && c->split) rc = hip_status(hipStreamSynchronize(c->restore_stream), "hipStreamSynchronize");
+  return rc;
+}
+
+int kvx_cache_counters(kvx_cache* c, int64_t* saved_blocks, int64_t* restored_blocks, int64_t* stream_waits) {
+  if (!c) return set_error(KVX_E_INVALID, "NULL cache");
+  if (saved_blocks) *saved_blocks = c->saved;
+  if (restored_blocks) *restored_blocks = c->restored;
+  if (stream_waits) *stream_waits = c->waits;
+  return KVX_OK;
+}
+
+}  // extern "C"

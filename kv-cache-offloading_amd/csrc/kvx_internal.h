@@ -1,0 +1,56 @@
+// Internal declarations shared by the kernel launchers and the C ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kvx.h"
+
+namespace kvx {
+
+// Blocks handled by one save/restore launch. The list travels in the kernel
+// argument segment (ids + entry addresses: 12 bytes per block), so a launch
+// needs no device-side index buffer and stays capturable in a HIP graph.
+constexpr int kMaxBatch = 128;
+
+struct BlockBatch {
+  int32_t n;
+  int32_t ids[kMaxBatch];
+  uint64_t entries[kMaxBatch];
+};
+
+// Launch-time geometry derived from kvx_block_layout.
+struct PlaneGeom {
+  int64_t plane_stride;  // elements
+  int64_t block_stride;  // elements
+  int64_t scale_offset;  // bytes from an entry's payload to its scales
+  int32_t planes;
+  int32_t plane_rows;
+  int32_t head_dim;
+  int32_t chunks;        // tiles per plane
+};
+
+// Records a message for kvx_last_error() and returns `code`.
+int set_error(int code, const char* fmt, ...);
+// Converts a HIP status into the ABI convention, recording a message.
+int hip_status(hipError_t err, const char* what);
+
+int check_layout(const kvx_block_layout* layout, int32_t format);
+
+// Kernel launchers: arguments are validated by the caller.
+// `vector_ok`: the pool base, both strides and every entry allow 16-byte
+// vector access; otherwise the element-granular kernels run.
+hipError_t launch_save(const void* pool, const kvx_block_layout& layout, int32_t format,
+                       const BlockBatch& batch, int64_t scale_offset, bool vector_ok, hipStream_t stream);
+hipError_t launch_restore(void* pool, const kvx_block_layout& layout, int32_t format,
+                          const BlockBatch& batch, int64_t scale_offset, bool vector_ok, hipStream_t stream);
+// True when 16-byte vector kernels may address this pool/entry combination.
+bool vector_access_ok(const void* pool, const kvx_block_layout& layout, const uint64_t* entries, int32_t n);
+hipError_t launch_store_kvcache(const void* key, int64_t key_stride, const void* value,
+                                int64_t value_stride, void* k_cache, void* v_cache,
+                                const int32_t* slot_mapping, int64_t num_tokens, int64_t row_elems,
+                                int32_t elem_bytes, int64_t cache_slots, hipStream_t stream);
+hipError_t launch_sleep(hipStream_t stream, int64_t microseconds);
+hipError_t launch_selftest(uint64_t* counters, hipStream_t stream);
+
+}  // namespace kvx

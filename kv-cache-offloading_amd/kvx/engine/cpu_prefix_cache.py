@@ -1,0 +1,486 @@
+"""Bounded pinned-host KV block store with optional automatic preservation.
+
+Drop-in for CPUBlockCache of nanovllm/engine/cpu_prefix_cache.py: the same
+constructor, properties, errors, budget and slot bookkeeping, and the same
+duck-typed hooks the BlockManager calls. Data movement and its ordering run
+in libkvx (include/kvx.h): a native copy engine owns the save stream and, with
+split_streams=True, a separate restore stream; it gathers (and FP8-quantises)
+a pool block into device staging with one kernel and moves it to its pinned
+host slot with one DMA, and the reverse on restore. Per-block and per-slot
+events order save -> restore -> slot reuse against the caller's current
+stream without host synchronisation.
+
+Call from the engine-owning thread between steps (no locking), as the
+reference requires. The KV pool must be on a ROCm device: there is no
+torch-op path for CPU-resident pools.
+"""
+
+import ctypes
+from dataclasses import dataclass
+from math import prod
+
+import torch
+
+from kvx import _lib, ops
+from kvx._lib import check, int32_array, lib
+from kvx.engine.block_manager import BlockManager
+
+# Pinned memory is allocated in chunks of about this size so one page-locking
+# call covers many entries (cpu_prefix_cache.py:11-13).
+_SLAB_CHUNK_BYTES = 1 << 30
+
+# Device staging per copy stream: entries of one save/restore batch.
+_STAGING_BYTES = 256 << 20
+_MAX_BATCH = 128  # kMaxBatch in the library
+
+# The codec operators live in this module in the reference (cpu_prefix_cache.py:20-28).
+fp8_quantize = ops.fp8_quantize
+fp8_dequantize = ops.fp8_dequantize
+
+
+@dataclass(frozen=True)
+class _CPUBlock:
+    token_ids: tuple[int, ...]
+    kv: torch.Tensor  # [K/V, layer, token, KV head, head dim], a slab slot view
+    slot: int
+    scale: torch.Tensor | None = None  # FP8 only: [K/V, layer, token, KV head, 1]
+    saved: bool = False  # a save into `slot` was queued (its event lives in the copy engine)
+
+
+class CPUCacheFullError(MemoryError):
+    """The configured payload budget cannot admit another block."""
+
+
+class _CopyEngine:
+    """Owner of one kvx_cache handle (streams, events, slab/staging registry)."""
+
+    def __init__(self, pool: torch.Tensor, layout, fmt: int, split: bool):
+        self.layout, self.fmt = layout, fmt
+        self.logical_bytes, self.scale_offset, self.entry_stride = ops.entry_layout(layout, fmt)
+        handle = ctypes.c_void_p()
+        check(lib().kvx_cache_create(pool.data_ptr(), ctypes.byref(layout), fmt, int(split), pool.device.index,
+                                     ctypes.byref(handle)), "kvx_cache_create")
+        self.handle = handle
+        save, restore = ctypes.c_void_p(), ctypes.c_void_p()
+        check(lib().kvx_cache_streams(handle, ctypes.byref(save), ctypes.byref(restore)), "kvx_cache_streams")
+        self.save_stream = torch.cuda.ExternalStream(save.value or 0, device=pool.device)
+        self.restore_stream = (self.save_stream if restore.value == save.value
+                               else torch.cuda.ExternalStream(restore.value or 0, device=pool.device))
+
+    def set_staging(self, save: torch.Tensor, restore: torch.Tensor, entries: int):
+        check(lib().kvx_cache_set_staging(self.handle, save.data_ptr(), restore.data_ptr(), entries), "staging")
+
+    def add_slab(self, slab: torch.Tensor, count: int):
+        check(lib().kvx_cache_add_slab(self.handle, slab.data_ptr(), count), "kvx_cache_add_slab")
+
+    def save(self, block_ids, slots, compute: int):
+        check(lib().kvx_cache_save(self.handle, int32_array(block_ids), int32_array(slots), len(block_ids),
+                                   compute), "kvx_cache_save")
+
+    def restore(self, slots, block_ids, wait: bool, compute: int):
+        check(lib().kvx_cache_restore(self.handle, int32_array(slots), int32_array(block_ids), len(slots),
+                                      int(wait), compute), "kvx_cache_restore")
+
+    def before_block_reuse(self, block_id: int, compute: int):
+        check(lib().kvx_cache_before_block_reuse(self.handle, block_id, compute), "before_block_reuse")
+
+    def before_block_use(self, block_id: int, compute: int):
+        check(lib().kvx_cache_before_block_use(self.handle, block_id, compute), "before_block_use")
+
+    def synchronize(self):
+        check(lib().kvx_cache_synchronize(self.handle), "kvx_cache_synchronize")
+
+    def counters(self) -> dict[str, int]:
+        vals = [ctypes.c_int64() for _ in range(3)]
+        check(lib().kvx_cache_counters(self.handle, *map(ctypes.byref, vals)), "kvx_cache_counters")
+        return dict(zip(("saved_blocks", "restored_blocks", "stream_waits"), (v.value for v in vals)))
+
+    def reset_slabs(self):
+        check(lib().kvx_cache_reset_slabs(self.handle), "kvx_cache_reset_slabs")
+
+    def close(self):
+        if self.handle:
+            handle, self.handle = self.handle, None
+            check(lib().kvx_cache_destroy(handle), "kvx_cache_destroy")
+
+
+class CPUBlockCache:
+    """One engine's bounded payload store, with optional automatic integration.
+
+    Keys are the engine's chained prefix hashes, not physical block IDs. The
+    byte budget covers tensor payloads (plus FP8 scales), not Python
+    metadata. Restored GPU entries are recyclable, not pinned; the CPU copy
+    survives until discard/clear/close. Behaviour of every option follows
+    cpu_prefix_cache.py:44-70: save_on_release saves a published block when
+    its last owner releases it while admission is blocked; prefetch restores
+    a blocked request's CPU hits into spare blocks in the background; fp8
+    stores float8_e4m3fn payloads with one scale per (token, KV head) row in
+    `scale_dtype` (default: the pool dtype, as the reference); hybrid =
+    (restore_s_per_block, recompute_s_per_token, recompute_s_per_token2)
+    lets admission recompute a CPU-only prefix's head while its tail restores.
+    Call synchronize() before reading payloads on the host.
+    """
+
+    def __init__(self, runner, block_manager: BlockManager, max_bytes: int, *,
+                 automatic: bool = False, save_on_release: bool = False, preallocate: bool = False,
+                 prefetch: bool = False, split_streams: bool = False, fp8: bool = False,
+                 hybrid: tuple[float, float, float] | None = None, scale_dtype: torch.dtype | None = None):
+        if type(max_bytes) is not int or max_bytes <= 0:
+            raise ValueError("max_bytes must be a positive integer")
+        if runner.world_size != 1:
+            raise NotImplementedError("CPU prefix blocks currently require TP=1")
+        if (save_on_release or prefetch or hybrid) and not automatic:
+            raise ValueError("save_on_release, prefetch and hybrid require automatic=True")
+        if hybrid is not None and (len(hybrid) != 3 or min(hybrid) < 0):
+            raise ValueError("hybrid needs three nonnegative cost coefficients")
+        cache = runner.kv_cache
+        if (cache.ndim != 6 or cache.shape[0] != 2 or min(cache.shape) <= 0
+                or cache.shape[2] != len(block_manager.blocks)
+                or cache.shape[3] != block_manager.block_size
+                or runner.block_size != block_manager.block_size):
+            raise ValueError("KV pool layout does not match the block manager")
+        if cache.device.type != "cuda":
+            raise ValueError("KV pool must be on a ROCm device (libkvx copies blocks with HIP kernels)")
+        if not cache.is_contiguous():
+            raise ValueError("KV pool must be contiguous")
+        scale_dtype = cache.dtype if scale_dtype is None else scale_dtype
+        if fp8 and (cache.dtype != torch.bfloat16 or scale_dtype not in ops.SCALE_DTYPES):
+            raise NotImplementedError("FP8 payloads need a bfloat16 pool and a bfloat16/float32 scale")
+        self._cache = cache
+        self._manager = block_manager
+        self._shape = (2, cache.shape[1], *cache.shape[3:])
+        self._fp8 = fp8
+        self._dtype = torch.float8_e4m3fn if fp8 else cache.dtype
+        self._scale_dtype = scale_dtype
+        self._scale_shape = (*self._shape[:-1], 1)
+        self._block_bytes = prod(self._shape) * self._dtype.itemsize
+        if fp8:
+            self._block_bytes += prod(self._scale_shape) * scale_dtype.itemsize
+        self._max_bytes = max_bytes
+        self._entries: dict[int, _CPUBlock] = {}
+        self._capacity = max_bytes // self._block_bytes
+        self._slabs: list[torch.Tensor] = []  # payload views [count, 2, L, BS, H, hd]
+        self._scale_slabs: list[torch.Tensor] = []  # FP8 scale views [count, 2, L, BS, H, 1]
+        self._slab_memory: list[torch.Tensor] = []  # the pinned allocations
+        self._free_slots: list[int] = []
+        self._num_slots = 0
+        self._hybrid = hybrid
+        self._save_on_release = save_on_release
+        self._prefetch = prefetch
+        self._prefetched_blocks = 0
+        self._saved_blocks = 0
+        self._restored_blocks = 0
+        self._budget_skips = 0
+        self._layout = ops.pool_layout(cache, scale_dtype)
+        fmt = ops.FORMAT_FP8 if fp8 else ops.FORMAT_RAW
+        self._engine = _CopyEngine(cache, self._layout, fmt, split_streams)
+        assert self._engine.logical_bytes == self._block_bytes
+        self._copy_stream = self._engine.save_stream
+        self._restore_stream = self._engine.restore_stream
+        self._staging: list[torch.Tensor] = []
+        if automatic:
+            if block_manager._cpu_prefix_cache is not None:
+                self._engine.close()
+                raise RuntimeError("block manager already has an automatic CPU cache")
+            block_manager._cpu_prefix_cache = self
+        if preallocate:
+            while self._num_slots < self._capacity:
+                self._grow()
+
+    # -- properties (cpu_prefix_cache.py:133-193) --------------------------
+
+    @property
+    def max_bytes(self) -> int:
+        return self._max_bytes
+
+    @property
+    def block_bytes(self) -> int:
+        return self._block_bytes
+
+    @property
+    def bytes_used(self) -> int:
+        return len(self._entries) * self._block_bytes
+
+    @property
+    def reserved_bytes(self) -> int:
+        return self._num_slots * self._block_bytes
+
+    @property
+    def closed(self) -> bool:
+        return self._cache is None
+
+    @property
+    def automatic(self) -> bool:
+        return not self.closed and self._manager._cpu_prefix_cache is self
+
+    @property
+    def prefetch_enabled(self) -> bool:
+        return self._prefetch
+
+    @property
+    def hybrid(self) -> tuple[float, float, float] | None:
+        return self._hybrid
+
+    @hybrid.setter
+    def hybrid(self, costs: tuple[float, float, float] | None):
+        """Set split-admission costs, e.g. after measure_restore_s_per_block()."""
+        if costs is not None:
+            if not self.automatic:
+                raise ValueError("hybrid requires an automatic cache")
+            if len(costs) != 3 or min(costs) < 0:
+                raise ValueError("hybrid needs three nonnegative cost coefficients")
+            costs = tuple(float(c) for c in costs)
+        self._hybrid = costs
+
+    @property
+    def fp8(self) -> bool:
+        return self._fp8
+
+    @property
+    def prefetched_blocks(self) -> int:
+        return self._prefetched_blocks
+
+    @property
+    def stats(self) -> dict[str, int]:
+        return {"saved_blocks": self._saved_blocks, "restored_blocks": self._restored_blocks,
+                "budget_skips": self._budget_skips}
+
+    def __len__(self):
+        return len(self._entries)
+
+    def __contains__(self, prefix_hash: int):
+        return prefix_hash in self._entries
+
+    def _require_open(self):
+        if self.closed:
+            raise RuntimeError("CPU prefix cache is closed")
+
+    # -- host slabs and device staging -------------------------------------
+
+    def _grow(self):
+        """Pin one more chunk of slots (cpu_prefix_cache.py:199-208); LIFO free list, lowest slot first."""
+        count = min(max(1, _SLAB_CHUNK_BYTES // self._block_bytes), self._capacity - self._num_slots)
+        stride = self._engine.entry_stride
+        memory = torch.empty(count * stride, dtype=torch.uint8, device="cpu", pin_memory=True)
+        rows = memory.view(count, stride)
+        payload_bytes = prod(self._shape) * self._dtype.itemsize
+        payload = rows[:, :payload_bytes].view(self._dtype).view(count, *self._shape)
+        scale = None
+        if self._fp8:
+            offset = self._engine.scale_offset
+            nbytes = prod(self._scale_shape) * self._scale_dtype.itemsize
+            scale = rows[:, offset:offset + nbytes].view(self._scale_dtype).view(count, *self._scale_shape)
+        self._engine.add_slab(memory, count)
+        self._slab_memory.append(memory)
+        self._slabs.append(payload)
+        if scale is not None:
+            self._scale_slabs.append(scale)
+        self._free_slots.extend(range(self._num_slots + count - 1, self._num_slots - 1, -1))
+        self._num_slots += count
+
+    def _slot_view(self, slot: int) -> tuple[torch.Tensor, torch.Tensor | None]:
+        for i, slab in enumerate(self._slabs):
+            if slot < len(slab):
+                return slab[slot], self._scale_slabs[i][slot] if self._fp8 else None
+            slot -= len(slab)
+        raise IndexError(slot)
+
+    def _ensure_staging(self):
+        if self._staging:
+            return
+        stride = self._engine.entry_stride
+        entries = max(1, min(_MAX_BATCH, _STAGING_BYTES // stride))
+        device = self._cache.device
+        save = torch.empty(entries * stride, dtype=torch.uint8, device=device)
+        restore = save
+        if self._restore_stream is not self._copy_stream:
+            restore = torch.empty(entries * stride, dtype=torch.uint8, device=device)
+        self._engine.set_staging(save, restore, entries)
+        self._staging = [save, restore]
+
+    def _compute_stream(self) -> int:
+        return torch.cuda.current_stream(self._cache.device).cuda_stream
+
+    # -- copies -------------------------------------------------------------
+
+    def measure_restore_s_per_block(self, repeats: int = 8) -> float:
+        """Time this cache's restore path (H2D DMA plus FP8 dequantisation) on scratch buffers.
+
+        Restores `repeats` zero entries into a one-block scratch pool through a
+        scratch copy engine of the same format, twice (the first pass warms up
+        clocks), and returns seconds per block of the second pass
+        (cpu_prefix_cache.py:245-268).
+        """
+        self._require_open()
+        device = self._cache.device
+        scratch = torch.empty((2, self._shape[1], 1, *self._shape[2:]), dtype=self._cache.dtype, device=device)
+        layout = ops.pool_layout(scratch, self._scale_dtype)
+        engine = _CopyEngine(scratch, layout, ops.FORMAT_FP8 if self._fp8 else ops.FORMAT_RAW, False)
+        try:
+            host = torch.zeros(repeats * engine.entry_stride, dtype=torch.uint8, pin_memory=True)
+            staging = torch.empty(engine.entry_stride, dtype=torch.uint8, device=device)
+            engine.add_slab(host, repeats)
+            engine.set_staging(staging, staging, 1)
+            stream = engine.restore_stream
+            compute = torch.cuda.current_stream(device)
+            for _ in range(2):
+                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                start.record(stream)
+                for i in range(repeats):
+                    engine.restore([i], [0], False, compute.cuda_stream)
+                end.record(stream)
+                end.synchronize()
+            return start.elapsed_time(end) / 1000 / repeats
+        finally:
+            engine.close()
+
+    def synchronize(self):
+        """Wait for every pending host<->device copy (needed before host reads)."""
+        if not self.closed:
+            self._engine.synchronize()
+
+    def _save_to_slot(self, block_id: int, slot: int):
+        """Queue pool block -> host slot on the save stream (the seam failure-injection tests patch)."""
+        self._ensure_staging()
+        self._engine.save([block_id], [slot], self._compute_stream())
+
+    def _restore_from_slot(self, slot: int, block_id: int, wait: bool):
+        """Queue host slot -> pool block on the restore stream."""
+        self._ensure_staging()
+        self._engine.restore([slot], [block_id], wait, self._compute_stream())
+
+    def save_block(self, prefix_hash: int) -> bool:
+        """Save a published full block; return False if already saved (cpu_prefix_cache.py:275-332).
+
+        A full budget raises CPUCacheFullError before any allocation. A copy
+        or allocation failure leaves CPU entries and GPU metadata unchanged.
+        Partial tails cannot be saved.
+        """
+        self._require_open()
+        entry = self._entries.get(prefix_hash)
+        block_id = self._manager.hash_to_block_id.get(prefix_hash)
+        if block_id is None:
+            if entry is not None:
+                return False
+            raise KeyError(f"GPU prefix block {prefix_hash} is not cached")
+        block = self._manager.blocks[block_id]
+        tokens = tuple(block.token_ids)
+        if block.hash != prefix_hash or len(tokens) != self._manager.block_size:
+            raise ValueError("source must be a published full prefix block")
+        if entry is not None:
+            if entry.token_ids != tokens:
+                raise ValueError("prefix hash has conflicting token metadata")
+            return False
+        if self.bytes_used + self.block_bytes > self.max_bytes:
+            raise CPUCacheFullError("CPU prefix cache payload budget exceeded")
+        if not self._free_slots:
+            self._grow()
+        slot = self._free_slots.pop()
+        try:
+            payload, scale = self._slot_view(slot)
+            self._save_to_slot(block_id, slot)
+        except BaseException:
+            self._free_slots.append(slot)
+            raise
+        self._entries[prefix_hash] = _CPUBlock(tokens, payload, slot, scale, True)
+        self._saved_blocks += 1
+        return True
+
+    def _preserve(self, prefix_hash: int):
+        # Only a budget miss is an expected fallback; device and allocation
+        # failures stay visible (cpu_prefix_cache.py:334-340).
+        try:
+            self.save_block(prefix_hash)
+        except CPUCacheFullError:
+            self._budget_skips += 1
+
+    def _preserve_before_recycle(self, prefix_hash: int):
+        self._preserve(prefix_hash)
+
+    def _preserve_on_release(self, prefix_hash: int):
+        # Only when a request is waiting for blocks: otherwise the block likely
+        # stays a GPU hit and the D2H traffic would only delay later copies.
+        if self._save_on_release and self._manager.admission_blocked:
+            self._preserve(prefix_hash)
+
+    def before_block_reuse(self, block_id: int):
+        """Order later writes to a GPU block after its pending save and restore, without a host sync."""
+        self._engine.before_block_reuse(block_id, self._compute_stream())
+
+    def before_block_use(self, block_id: int):
+        """Order later reads of a prefetched GPU block after its restore."""
+        self._engine.before_block_use(block_id, self._compute_stream())
+
+    def _entry_for(self, prefix_hash: int, token_ids):
+        """Pure lookup used while planning admission."""
+        entry = self._entries.get(prefix_hash)
+        return entry if entry is not None and entry.token_ids == tuple(token_ids) else None
+
+    def _copy_entry(self, entry: _CPUBlock, block_id: int, wait: bool = True):
+        """Restore `entry` into GPU block `block_id` (cpu_prefix_cache.py:370-398).
+
+        With wait=True the current stream waits for the copy; otherwise the
+        block stays pending until before_block_use/before_block_reuse.
+        """
+        self._require_open()
+        self._restore_from_slot(entry.slot, block_id, wait)
+        self._restored_blocks += 1
+
+    def restore_block(self, prefix_hash: int) -> int:
+        """Restore a CPU hit; return the GPU cache's physical block ID (cpu_prefix_cache.py:400-414).
+
+        GPU hits are reused without copying. On copy failure the destination
+        is freed and the hash stays unpublished; the CPU entry remains for a
+        retry.
+        """
+        self._require_open()
+        entry = self._entries[prefix_hash]
+
+        def copy_to_block(block_id):
+            self._copy_entry(entry, block_id)
+
+        return self._manager.restore_cached_block(prefix_hash, entry.token_ids, copy_to_block)
+
+    def discard(self, prefix_hash: int) -> bool:
+        """Release one CPU payload without changing GPU cache state.
+
+        A later save into the freed slot is ordered after restores still
+        reading it by the copy engine's per-slot events.
+        """
+        self._require_open()
+        entry = self._entries.pop(prefix_hash, None)
+        if entry is None:
+            return False
+        self._free_slots.append(entry.slot)
+        return True
+
+    def clear(self):
+        for entry in self._entries.values():
+            self._free_slots.append(entry.slot)
+        self._entries.clear()
+
+    def close(self):
+        """Release payloads, streams and pool references; idempotent."""
+        if self.closed:
+            return
+        if self.automatic:
+            self._manager._cpu_prefix_cache = None
+        self.synchronize()
+        self.clear()
+        self._engine.close()
+        self._staging.clear()
+        self._slabs.clear()
+        self._scale_slabs.clear()
+        self._slab_memory.clear()
+        self._free_slots.clear()
+        self._num_slots = 0
+        self._cache = None
+        self._manager = None
+
+    def __del__(self):
+        engine = getattr(self, "_engine", None)
+        if engine is not None and engine.handle:
+            try:
+                engine.close()
+            except Exception:
+                pass

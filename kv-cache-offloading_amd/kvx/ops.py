@@ -1,0 +1,217 @@
+"""Operator API of the KV-block copy path, backed by libkvx's HIP kernels.
+
+These functions keep the reference's names, argument meaning and out-param
+style (nanovllm/layers/attention.py:33-40, nanovllm/engine/cpu_prefix_cache.py:20-28)
+and accept the same tensors. Work is queued on torch's current HIP stream of
+the tensors' device. Tensors must live on a ROCm device: there is no CPU or
+torch-op fallback, so a missing or unloadable libkvx raises.
+"""
+
+import ctypes
+from math import prod
+
+import torch
+
+from kvx import _lib
+from kvx._lib import BlockLayout, check, int32_array, lib, uint64_array
+
+FORMAT_RAW, FORMAT_FP8 = _lib.FORMAT_RAW, _lib.FORMAT_FP8
+SCALE_DTYPES = {torch.bfloat16: _lib.SCALE_BF16, torch.float32: _lib.SCALE_FP32}
+
+# Largest finite float8_e4m3fn magnitude (the codec's clamp bound).
+FP8_MAX = 448.0
+
+
+def _require_device(*tensors: torch.Tensor) -> torch.device:
+    device = tensors[0].device
+    for t in tensors:
+        if t.device.type != "cuda":
+            raise ValueError("kvx operators need tensors on a ROCm device (got %s)" % t.device)
+        if t.device != device:
+            raise ValueError("kvx operators need all tensors on one device")
+    return device
+
+
+def _stream(device: torch.device, stream=None) -> int:
+    if stream is None:
+        stream = torch.cuda.current_stream(device)
+    return stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream)
+
+
+def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                  slot_mapping: torch.Tensor):
+    """Slot-mapped paged KV write (nanovllm/layers/attention.py:33-40).
+
+    key/value: [N, num_heads, head_dim] with contiguous rows (the row stride
+    may differ, e.g. V is a view of a fused QKV output). k_cache/v_cache:
+    contiguous [num_blocks, block_size, num_heads, head_dim] layer views of
+    the pool. slot_mapping: int32 [N]; -1 (graph padding) skips a token, and
+    so does any slot outside the cache. Capturable in a HIP graph.
+    """
+    N, num_heads, head_dim = key.shape
+    D = num_heads * head_dim
+    assert key.stride(-1) == 1 and value.stride(-1) == 1
+    assert key.stride(1) == head_dim and value.stride(1) == head_dim
+    assert k_cache.stride(1) == D and v_cache.stride(1) == D
+    assert slot_mapping.numel() == N
+    if value.shape != key.shape:
+        raise ValueError("key and value shapes differ")
+    if not (key.dtype == value.dtype == k_cache.dtype == v_cache.dtype):
+        raise TypeError("key, value and caches must share one dtype")
+    if slot_mapping.dtype != torch.int32 or not slot_mapping.is_contiguous():
+        raise TypeError("slot_mapping must be a contiguous int32 tensor")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()) or k_cache.numel() != v_cache.numel():
+        raise ValueError("k_cache and v_cache must be equally sized contiguous slot arrays")
+    device = _require_device(key, value, k_cache, v_cache, slot_mapping)
+    if N == 0:
+        return
+    check(lib().kvx_store_kvcache(key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0),
+                                  k_cache.data_ptr(), v_cache.data_ptr(), slot_mapping.data_ptr(), N,
+                                  num_heads, head_dim, key.element_size(), k_cache.numel() // D,
+                                  _stream(device)), "store_kvcache")
+
+
+# ---------------------------------------------------------------------------
+# Views as [planes][plane_rows][head_dim]
+
+def _plane_views(t: torch.Tensor):
+    """Yields (tensor, planes, plane_rows, plane_stride) covering `t` in row-major order.
+
+    The rows (last dim) must be contiguous. A view whose leading dims do not
+    collapse into one uniformly strided plane dimension is split along its
+    first dim.
+    """
+    if t.stride(-1) != 1 and t.shape[-1] > 1:
+        raise ValueError("the last dim (head_dim) must be contiguous")
+    hd = t.shape[-1]
+    sizes, strides = list(t.shape[:-1]), list(t.stride()[:-1])
+    dims = [(s, st) for s, st in zip(sizes, strides) if s != 1]
+    # Longest suffix of dims whose rows are packed back to back.
+    rows, expect, k = 1, hd, len(dims)
+    while k > 0 and dims[k - 1][1] == expect:
+        rows *= dims[k - 1][0]
+        expect *= dims[k - 1][0]
+        k -= 1
+    lead = dims[:k]
+    collapsible = all(lead[i][1] == lead[i + 1][1] * lead[i + 1][0] for i in range(len(lead) - 1))
+    if collapsible:
+        planes = prod(s for s, _ in lead) if lead else 1
+        plane_stride = lead[-1][1] if lead else rows * hd
+        yield t, planes, rows, plane_stride
+        return
+    for i in range(t.shape[0]):
+        yield from _plane_views(t[i])
+
+
+def _check_codec(values: torch.Tensor, payload: torch.Tensor, scale: torch.Tensor):
+    if values.dtype != torch.bfloat16:
+        raise NotImplementedError("the FP8 codec supports bfloat16 KV values")
+    if payload.dtype != torch.float8_e4m3fn or payload.shape != values.shape or not payload.is_contiguous():
+        raise ValueError("payload must be a contiguous float8_e4m3fn tensor shaped like the values")
+    if scale.dtype not in SCALE_DTYPES or not scale.is_contiguous() or \
+            tuple(scale.shape) != (*values.shape[:-1], 1):
+        raise ValueError("scale must be a contiguous bfloat16/float32 tensor shaped [..., 1]")
+
+
+def _codec(save: bool, values: torch.Tensor, payload: torch.Tensor, scale: torch.Tensor):
+    _check_codec(values, payload, scale)
+    device = _require_device(values, payload, scale)
+    if values.numel() == 0:
+        return
+    hd = values.shape[-1]
+    stream = _stream(device)
+    scale_bytes = scale.element_size()
+    row = 0
+    fn = lib().kvx_save_blocks if save else lib().kvx_restore_blocks
+    for view, planes, rows, plane_stride in _plane_views(values):
+        layout = BlockLayout(plane_stride, 0, planes, rows, hd, 1, 2, SCALE_DTYPES[scale.dtype])
+        entry = payload.data_ptr() + row * hd
+        scale_offset = scale.data_ptr() + row * scale_bytes - entry
+        check(fn(view.data_ptr(), ctypes.byref(layout), FORMAT_FP8, int32_array([0]), uint64_array([entry]), 1,
+                 scale_offset, stream), "fp8_quantize" if save else "fp8_dequantize")
+        row += planes * rows
+
+
+def fp8_quantize(source: torch.Tensor, payload: torch.Tensor, scale: torch.Tensor):
+    """float8_e4m3fn payload with one scale (scale's dtype) per vector along the last dim.
+
+    Same contract as nanovllm/engine/cpu_prefix_cache.py:20-24:
+    scale = max(fp32(amax|x|) / 448, 1e-30) in scale's dtype, then
+    payload = e4m3(clamp(fp32(x) / fp32(scale), -448, 448)). `source` may be a
+    strided view (e.g. pool[:, :, block]); payload and scale are contiguous.
+    """
+    _codec(True, source, payload, scale)
+
+
+def fp8_dequantize(payload: torch.Tensor, scale: torch.Tensor, target: torch.Tensor):
+    """target = bf16(fp32(payload) * fp32(scale)) (nanovllm/engine/cpu_prefix_cache.py:27-28)."""
+    _codec(False, target, payload, scale)
+
+
+# ---------------------------------------------------------------------------
+# Pool block lists
+
+def pool_layout(pool: torch.Tensor, scale_dtype: torch.dtype | None = None) -> BlockLayout:
+    """kvx_block_layout of a contiguous [2, L, NB, BS, H, hd] pool (model_runner.py:120)."""
+    if pool.ndim != 6 or pool.shape[0] != 2 or not pool.is_contiguous():
+        raise ValueError("pool must be a contiguous [2, layers, blocks, block_size, heads, head_dim] tensor")
+    _, layers, nb, bs, heads, hd = pool.shape
+    scale = SCALE_DTYPES.get(scale_dtype if scale_dtype is not None else pool.dtype, _lib.SCALE_BF16)
+    return BlockLayout(nb * bs * heads * hd, bs * heads * hd, 2 * layers, bs * heads, hd, nb,
+                       pool.element_size(), scale)
+
+
+def entry_layout(layout: BlockLayout, fmt: int) -> tuple[int, int, int]:
+    """(logical bytes, scale offset, entry stride) of one host entry."""
+    logical, offset, stride = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    check(lib().kvx_entry_layout(ctypes.byref(layout), fmt, ctypes.byref(logical), ctypes.byref(offset),
+                                 ctypes.byref(stride)), "entry_layout")
+    return logical.value, offset.value, stride.value
+
+
+def save_blocks(pool: torch.Tensor, block_ids, entries, fmt: int, scale_dtype: torch.dtype | None = None,
+                stream=None):
+    """Queues save (gather [+ FP8 quantise]) of pool blocks into entry addresses."""
+    layout = pool_layout(pool, scale_dtype)
+    _, offset, _ = entry_layout(layout, fmt)
+    ids, entries = list(block_ids), list(entries)
+    if len(ids) != len(entries):
+        raise ValueError("one entry per block")
+    device = _require_device(pool)
+    check(lib().kvx_save_blocks(pool.data_ptr(), ctypes.byref(layout), fmt, int32_array(ids),
+                                uint64_array(entries), len(ids), offset, _stream(device, stream)), "save_blocks")
+
+
+def restore_blocks(pool: torch.Tensor, block_ids, entries, fmt: int, scale_dtype: torch.dtype | None = None,
+                   stream=None):
+    """Queues restore ([FP8 dequantise +] scatter) of entry addresses into pool blocks."""
+    layout = pool_layout(pool, scale_dtype)
+    _, offset, _ = entry_layout(layout, fmt)
+    ids, entries = list(block_ids), list(entries)
+    if len(ids) != len(entries):
+        raise ValueError("one entry per block")
+    device = _require_device(pool)
+    check(lib().kvx_restore_blocks(pool.data_ptr(), ctypes.byref(layout), fmt, int32_array(ids),
+                                   uint64_array(entries), len(ids), offset, _stream(device, stream)),
+          "restore_blocks")
+
+
+# ---------------------------------------------------------------------------
+# Test hooks
+
+def sleep(microseconds: int, stream=None, device=None):
+    """Queues a bounded busy wait on `stream` (torch's current stream by default)."""
+    device = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    check(lib().kvx_sleep(_stream(device, stream), int(microseconds)), "sleep")
+
+
+SELFTEST_FIELDS = ("e4m3_encode_mismatch", "bf16_round_mismatch", "nan_not_preserved", "division_mismatch",
+                   "e4m3_decode_mismatch", "encode_inputs_2p20", "division_pairs_2p20", "decode_sweeps")
+
+
+def selftest(device=None) -> dict[str, int]:
+    """Runs libkvx's exhaustive device self-test; returns its counters by name."""
+    device = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    counters = torch.zeros(8, dtype=torch.int64, device=device)
+    check(lib().kvx_selftest(counters.data_ptr(), _stream(device)), "selftest")
+    return dict(zip(SELFTEST_FIELDS, counters.cpu().tolist()))

@@ -1,0 +1,266 @@
+"""CPUBlockCache over libkvx's copy engine, restating the reference's cache tests on a ROCm pool.
+
+Sources: bench/test_cpu_prefix_cache.py, bench/test_cpu_cache_optimizations.py and
+bench/test_automatic_cpu_cache.py. The reference drives these through its engine
+with a scripted model; here the block manager is driven directly (publishing
+blocks as a finished prefill would), which exercises the same cache hooks.
+Ordering is stressed the reference's way: a delay kernel queued on a copy
+stream before each copy (test_automatic_cpu_cache.py:37-51) and pinned slabs
+poisoned with 0xAB (test_cpu_cache_optimizations.py:83-86).
+"""
+
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bf16_bits, u8
+from kvx import ops
+from kvx.engine.block_manager import BlockManager
+from kvx.engine.cpu_prefix_cache import CPUBlockCache, CPUCacheFullError
+from oracle import kvx_oracle as oracle
+
+pytestmark = pytest.mark.gpu
+
+BS = 256
+DELAY_US = 20_000  # about torch.cuda._sleep(20_000_000) at ~1 GHz
+
+
+def make_pool(device, num_blocks, layers=2, heads=1, hd=4, pattern="bytes"):
+    """The reference fixtures' pool (2, 2, NB, 256, 1, 4) (test_engine_handoff.py:16)."""
+    pool = torch.empty((2, layers, num_blocks, BS, heads, hd), dtype=torch.bfloat16, device=device)
+    if pattern == "bytes":  # every bit pattern, NaNs included (test_cpu_prefix_cache.py:15-18)
+        raw = torch.arange(pool.numel() * 2, device=device).remainder(256).to(torch.uint8)
+        pool.view(torch.uint8).copy_(raw.view(pool.view(torch.uint8).shape))
+    else:  # finite values for FP8
+        g = torch.Generator(device=device).manual_seed(num_blocks)
+        pool.copy_(torch.randn(pool.shape, generator=g, device=device))
+    return pool
+
+
+def publish(manager: BlockManager, block_id: int, token: int, prefix: int = -1) -> int:
+    """Mark a GPU block as a finished, published full prefix block; return its hash."""
+    tokens = [token] * manager.block_size
+    h = manager.compute_hash(tokens, prefix)
+    manager.blocks[block_id].update(h, tokens)
+    manager.hash_to_block_id[h] = block_id
+    return h
+
+
+def forget(manager: BlockManager, key: int) -> int:
+    """Unpublish a GPU block without touching its bytes or ordering (test_cpu_cache_optimizations.py:90-94)."""
+    block_id = manager.hash_to_block_id.pop(key)
+    manager.blocks[block_id].hash, manager.blocks[block_id].token_ids = -1, []
+    return block_id
+
+
+def block_bytes(pool, block_id):
+    torch.cuda.synchronize()
+    return u8(pool[:, :, block_id])
+
+
+def new_cache(pool, manager, blocks=1, **kwargs):
+    runner = SimpleNamespace(world_size=1, block_size=BS, kv_cache=pool)
+    bf16_block = pool[:, :, 0].numel() * pool.element_size()
+    if kwargs.get("fp8"):
+        rows = pool[:, :, 0].numel() // pool.shape[-1]
+        size = pool[:, :, 0].numel() + rows * (kwargs.get("scale_dtype") or pool.dtype).itemsize
+    else:
+        size = bf16_block
+    return CPUBlockCache(runner, manager, blocks * size, **kwargs)
+
+
+def slow_copies(cache, names=("_save_to_slot", "_restore_from_slot")):
+    """Queue a delay on the copy stream before each copy so a missing wait corrupts bytes."""
+    streams = {"_save_to_slot": cache._copy_stream, "_restore_from_slot": cache._restore_stream}
+    for name in names:
+        original = getattr(cache, name)
+
+        def delayed(*args, _original=original, _stream=streams[name], **kwargs):
+            ops.sleep(DELAY_US, stream=_stream, device=cache._cache.device)
+            return _original(*args, **kwargs)
+
+        setattr(cache, name, delayed)
+
+
+@pytest.mark.parametrize("slow", [False, True])
+def test_round_trip_is_byte_exact_and_survives_pool_overwrite(gpu, slow):
+    pool = make_pool(gpu, 4)
+    manager = BlockManager(4, BS)
+    key = publish(manager, 1, 1)
+    expected = block_bytes(pool, 1)
+    cache = new_cache(pool, manager)
+    if slow:
+        slow_copies(cache)
+    assert cache.save_block(key)
+    assert key in cache and len(cache) == 1
+    assert cache.bytes_used == cache.block_bytes == cache.max_bytes
+    forget(manager, key)
+    # Overwrite the pool on the compute stream; before_block_reuse orders it after the save.
+    cache.before_block_reuse(1)
+    pool.fill_(-7)
+    target = cache.restore_block(key)
+    assert np.array_equal(block_bytes(pool, target), expected)
+    assert manager.blocks[target].ref_count == 0 and manager.hash_to_block_id[key] == target
+    cache.close()
+
+
+@pytest.mark.parametrize("scale_dtype", [None, torch.float32])
+def test_fp8_entry_is_bit_exact_and_restores_within_the_reference_bound(gpu, scale_dtype):
+    pool = make_pool(gpu, 3, layers=2, heads=8, hd=128, pattern="normal")
+    manager = BlockManager(3, BS)
+    key = publish(manager, 2, 5)
+    source = pool[:, :, 2].float().cpu()
+    host_pool = bf16_bits(pool)
+    cache = new_cache(pool, manager, blocks=4, fp8=True, scale_dtype=scale_dtype)
+    numel = pool[:, :, 0].numel()
+    sdtype = scale_dtype or pool.dtype
+    assert cache.block_bytes == numel + numel // pool.shape[-1] * sdtype.itemsize  # (:64)
+    assert cache.save_block(key)
+    cache.synchronize()
+    entry = cache._entries[key]
+    codes, scales = oracle.save_block_fp8(host_pool, 2, sdtype == torch.float32)
+    assert np.array_equal(u8(entry.kv), codes) and np.array_equal(u8(entry.scale), scales.view(np.uint8))
+    forget(manager, key)
+    cache.before_block_reuse(2)
+    pool[:, :, 2].zero_()
+    target = cache.restore_block(key)
+    cache.synchronize()
+    restored = pool[:, :, target].float().cpu()
+    bound = source.abs().amax(-1, keepdim=True) / 16  # test_cpu_cache_optimizations.py:71-73
+    assert torch.all((restored - source).abs() <= bound)
+    assert np.array_equal(bf16_bits(pool[:, :, target]), oracle.dequantize(codes, scales, sdtype == torch.float32))
+    assert cache.stats["restored_blocks"] == 1
+
+
+def split_cache(pool, manager, **kwargs):
+    cache = new_cache(pool, manager, split_streams=True, preallocate=True, **kwargs)
+    assert cache._restore_stream is not cache._copy_stream
+    for slab in cache._slab_memory:
+        slab.fill_(0xAB)
+    return cache
+
+
+@pytest.mark.parametrize("slow", [False, True])
+def test_split_streams_restore_waits_for_its_save(gpu, slow):
+    pool = make_pool(gpu, 3)
+    manager = BlockManager(3, BS)
+    key = publish(manager, 0, 1)
+    cache = split_cache(pool, manager)
+    if slow:
+        slow_copies(cache, ["_save_to_slot"])  # a fast restore would overtake a missing wait
+    expected = block_bytes(pool, 0)
+    assert cache.save_block(key)
+    forget(manager, key)
+    target = cache.restore_block(key)
+    cache.synchronize()
+    assert np.array_equal(block_bytes(pool, target), expected)
+
+
+@pytest.mark.parametrize("slow", [False, True])
+def test_split_streams_slot_reuse_waits_for_pending_restore(gpu, slow):
+    pool = make_pool(gpu, 3)
+    manager = BlockManager(3, BS)
+    key = publish(manager, 0, 1)
+    cache = split_cache(pool, manager)
+    expected = block_bytes(pool, 0)
+    assert cache.save_block(key)
+    cache.synchronize()
+    forget(manager, key)
+    if slow:
+        slow_copies(cache, ["_restore_from_slot"])  # a fast save would overwrite the slot first
+    entry = cache._entries[key]
+    target = manager.restore_cached_block(key, entry.token_ids,
+                                          lambda block_id: cache._copy_entry(entry, block_id, wait=False))
+    assert cache.discard(key)
+    other = next(i for i in range(3) if i != target)
+    pool[:, :, other].fill_(7)
+    other_key = publish(manager, other, 2)
+    assert cache.save_block(other_key)  # reuses the slot the restore may still read
+    cache.synchronize()
+    assert np.array_equal(block_bytes(pool, target), expected)
+    assert np.array_equal(u8(cache._slot_view(0)[0]), block_bytes(pool, other))
+
+
+def test_restore_into_a_recycled_victim_waits_for_the_victims_save(gpu):
+    # A prefetch-style restore allocates without write ordering
+    # (block_manager.py:168); if that recycles a published victim, the victim's
+    # save was queued just before. The copy engine orders the restore's writes
+    # after that save, so both the saved victim and the restored block are intact.
+    pool = make_pool(gpu, 2)
+    manager = BlockManager(2, BS)
+    victim_key = publish(manager, 0, 3)
+    key = publish(manager, 1, 4)
+    cache = new_cache(pool, manager, blocks=2, automatic=True, split_streams=True)
+    victim_bytes, expected = block_bytes(pool, 0), block_bytes(pool, 1)
+    assert cache.save_block(key)
+    cache.synchronize()
+    forget(manager, key)
+    assert list(manager.free_block_ids) == [0, 1]  # block 0 (the victim) recycles first
+    slow_copies(cache, ["_save_to_slot"])
+    entry = cache._entries[key]
+    target = manager.restore_cached_block(key, entry.token_ids,
+                                          lambda block_id: cache._copy_entry(entry, block_id, wait=False))
+    assert target == 0 and victim_key in cache
+    cache.before_block_use(target)
+    cache.synchronize()
+    assert np.array_equal(block_bytes(pool, 0), expected)
+    victim = cache._entries[victim_key]
+    assert np.array_equal(u8(victim.kv), victim_bytes)
+
+
+def test_budget_rules_dedup_discard_and_slot_reuse(gpu):
+    pool = make_pool(gpu, 3)
+    manager = BlockManager(3, BS)
+    key = publish(manager, 0, 1)
+    other = publish(manager, 1, 2)
+    cache = new_cache(pool, manager)
+    assert cache.reserved_bytes == 0
+    assert cache.save_block(key)
+    assert not cache.save_block(key)
+    assert cache.reserved_bytes == cache.block_bytes
+    with pytest.raises(CPUCacheFullError, match="budget"):
+        cache.save_block(other)
+    assert cache.discard(key) and not cache.discard(key)
+    assert cache.save_block(other)  # reuses the freed slot
+    assert cache.reserved_bytes == cache.bytes_used == cache.block_bytes
+    with pytest.raises(KeyError):
+        cache.save_block(-1)
+    cache.clear()
+    assert cache.bytes_used == len(cache) == 0 and other in manager.hash_to_block_id
+    cache.close()
+    cache.close()
+    assert cache.closed
+    with pytest.raises(RuntimeError, match="closed"):
+        cache.save_block(key)
+
+
+def test_preallocated_multi_slab_slots_round_trip(gpu, monkeypatch):
+    import kvx.engine.cpu_prefix_cache as module
+
+    monkeypatch.setattr(module, "_SLAB_CHUNK_BYTES", 1)
+    pool = make_pool(gpu, 4)
+    manager = BlockManager(4, BS)
+    keys = [publish(manager, b, 10 + b) for b in range(3)]
+    expected = {k: block_bytes(pool, manager.hash_to_block_id[k]) for k in keys}
+    cache = new_cache(pool, manager, blocks=3, preallocate=True)
+    assert len(cache._slabs) == 3 and cache.reserved_bytes == 3 * cache.block_bytes
+    for k in keys:
+        cache.save_block(k)
+    assert len({cache._entries[k].slot for k in keys}) == 3
+    cache.synchronize()
+    for k in keys:
+        forget(manager, k)
+    cache.before_block_reuse(0)
+    pool.fill_(0)
+    for k in keys:
+        restored = cache.restore_block(k)
+        assert np.array_equal(block_bytes(pool, restored), expected[k])
+
+
+def test_measure_restore_time_is_positive(gpu):
+    pool = make_pool(gpu, 2, layers=2, heads=8, hd=128, pattern="normal")
+    cache = new_cache(pool, BlockManager(2, BS), fp8=True)
+    seconds = cache.measure_restore_s_per_block(repeats=4)
+    assert 0 < seconds < 1
