@@ -20,6 +20,7 @@ Run: python bench.py [--steps 50] [--warmup 5] [--blocks 128]
 """
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -51,7 +52,22 @@ def parse_args():
     p.add_argument("--skip-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample budget")
     p.add_argument("--host-reps", type=int, default=3)
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="after timing, gather the same blocks once with the BF16 copy kernel (known bytes), "
+                        "to scale HBM counters read under rocprofv3 --pmc")
     return p.parse_args()
+
+
+def pmc_traffic(kernel_prefix: str):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 PMC summary, if one matches."""
+    path = ROOT / "profiles" / "fp8_save_restore_qwen3_8b.traffic.json"
+    if not path.exists():
+        return None, None
+    data = json.loads(path.read_text())
+    for name, entry in data["kernels"].items():
+        if name.startswith(kernel_prefix):
+            return entry["total_bytes"], data["source"]
+    return None, None
 
 
 def kernel_leg(torch, ops, pool, sources, dests, scale_dtype, steps, warmup):
@@ -132,21 +148,22 @@ def host_link_leg(torch, pool, layout, sources, dests, reps):
 
         both_s = timed(both)
 
-        # Ceiling: one contiguous pinned copy each way, and both at once on two streams.
+        # Ceiling: one contiguous pinned hipMemcpyAsync each way, and both at
+        # once, on the engine's two streams (the runtime torch loaded).
+        hip = ctypes.CDLL("libamdhip64.so.7")
+        hip.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
+                                       ctypes.c_void_p]
         flat_dev = torch.empty(link_bytes, dtype=torch.uint8, device=pool.device)
-        flat_host = slab[:link_bytes]
-        flat_host2 = slab[n * stride:n * stride + link_bytes]
-        s1, s2 = torch.cuda.Stream(pool.device), torch.cuda.Stream(pool.device)
+        flat_dev2 = torch.empty_like(flat_dev)
+        host_a, host_b = slab.data_ptr(), slab.data_ptr() + n * stride
+        s1, s2 = engine.save_stream.cuda_stream, engine.restore_stream.cuda_stream
 
         def d2h():
-            with torch.cuda.stream(s1):
-                flat_host.copy_(flat_dev, non_blocking=True)
+            assert hip.hipMemcpyAsync(host_a, flat_dev.data_ptr(), link_bytes, 2, s1) == 0
 
         def h2d():
-            with torch.cuda.stream(s2):
-                flat_dev2.copy_(flat_host2, non_blocking=True)
+            assert hip.hipMemcpyAsync(flat_dev2.data_ptr(), host_b, link_bytes, 1, s2) == 0
 
-        flat_dev2 = torch.empty_like(flat_dev)
         ceil_d2h = timed(d2h)
         ceil_h2d = timed(h2d)
         ceil_both = timed(lambda: (d2h(), h2d()))
@@ -236,6 +253,8 @@ def main():
     restore_gbs = k["hbm_bytes"] / (k["restore_ms"] / 1000) / 1e9
     dominant = "save" if k["save_ms"] >= k["restore_ms"] else "restore"
     achieved = min(save_gbs, restore_gbs)
+    scale_flag = "true" if args.scale == "bf16" else "false"
+    traffic, traffic_source = pmc_traffic(f"fp8_{dominant}_kernel<128, 2, 1, {scale_flag}>")
     log(f"step {ms_per_step:.3f} ms; save {k['save_ms']:.3f} ms ({save_gbs:.0f} GB/s), "
         f"restore {k['restore_ms']:.3f} ms ({restore_gbs:.0f} GB/s)")
 
@@ -270,7 +289,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_source,
         },
         "kernels": {
             "save": {"ms": round(k["save_ms"], 4), "hbm_gbs": round(save_gbs, 1),
@@ -280,6 +300,16 @@ def main():
             "algorithmic_bytes_per_launch": k["hbm_bytes"],
         },
     }
+    if args.calibrate_copy:
+        raw_layout = ops.pool_layout(pool)
+        _, _, raw_stride = ops.entry_layout(raw_layout, ops.FORMAT_RAW)
+        raw = torch.empty(args.blocks * raw_stride, dtype=torch.uint8, device=device)
+        ops.save_blocks(pool, sources, [raw.data_ptr() + i * raw_stride for i in range(args.blocks)],
+                        ops.FORMAT_RAW)
+        torch.cuda.synchronize()
+        result["calibration_copy"] = {"kernel": "raw_copy_kernel", "read_bytes": args.blocks * BF16_BLOCK_BYTES,
+                                      "write_bytes": args.blocks * BF16_BLOCK_BYTES}
+        del raw
     if not args.skip_host_link:
         log("host link leg")
         result["host_link"] = host_link_leg(torch, pool, ops.pool_layout(pool, scale_dtype), sources, dests,

@@ -128,16 +128,18 @@ int kvx_restore_blocks(void* pool, const kvx_block_layout* layout, int32_t forma
 /*
  * Copy engine: the stream/event half of CPUBlockCache
  * (nanovllm/engine/cpu_prefix_cache.py:72-131, 270-273, 306-322, 352-363,
- * 370-398). It owns a save stream and (split_streams != 0) a separate
- * restore stream, both at default priority, and per GPU block / host slot
- * events. Host slabs and device staging are owned by the caller.
+ * 370-398). It queues copies on a save stream and a restore stream that the
+ * caller creates and keeps alive (the reference uses torch.cuda.Stream,
+ * :110-113; pass the same stream twice for split_streams=False) and keeps
+ * per GPU block / host slot events. Host slabs and device staging are
+ * owned by the caller too; the engine never frees or destroys them.
  */
 typedef struct kvx_cache kvx_cache;
 
-/* Creates an engine for `pool` on `device` (cpu_prefix_cache.py:110-113). */
-int kvx_cache_create(void* pool, const kvx_block_layout* layout, int32_t format,
-                     int32_t split_streams, int32_t device, kvx_cache** out);
-/* Frees streams and events after synchronising both streams (:431-448). */
+/* Creates an engine for `pool` on `device` using the caller's two streams (non-NULL). */
+int kvx_cache_create(void* pool, const kvx_block_layout* layout, int32_t format, void* save_stream,
+                     void* restore_stream, int32_t device, kvx_cache** out);
+/* Synchronises both streams, then frees the engine's events (:431-448). */
 int kvx_cache_destroy(kvx_cache* cache);
 /*
  * Attaches one device staging area per stream, each holding `entries`
@@ -153,7 +155,7 @@ int kvx_cache_set_staging(kvx_cache* cache, void* save_staging, void* restore_st
 int kvx_cache_add_slab(kvx_cache* cache, void* host_base, int32_t count);
 /* Drops all slabs and per-slot events after synchronising (close, :431-448). */
 int kvx_cache_reset_slabs(kvx_cache* cache);
-/* hipStream_t of the save and restore streams (equal without split streams). */
+/* The save and restore streams the engine was created with (equal without split streams). */
 int kvx_cache_streams(kvx_cache* cache, void** save_stream, void** restore_stream);
 
 /*

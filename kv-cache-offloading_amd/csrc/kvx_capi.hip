@@ -322,13 +322,15 @@ int kvx_selftest(uint64_t* counters, void* stream) {
   return hip_status(launch_selftest(counters, (hipStream_t)stream), "selftest launch");
 }
 
-int kvx_cache_create(void* pool, const kvx_block_layout* layout, int32_t format, int32_t split_streams,
-                     int32_t device, kvx_cache** out) {
+int kvx_cache_create(void* pool, const kvx_block_layout* layout, int32_t format, void* save_stream,
+                     void* restore_stream, int32_t device, kvx_cache** out) {
   if (!out) return set_error(KVX_E_INVALID, "NULL output handle");
   *out = nullptr;
   int rc = check_layout(layout, format);
   if (rc) return rc;
   if (!pool || (uintptr_t)pool % 16) return set_error(KVX_E_INVALID, "pool must be a 16-byte aligned pointer");
+  if (!save_stream || !restore_stream)
+    return set_error(KVX_E_INVALID, "the copy engine needs two non-null streams (pass one twice to share it)");
   kvx_cache* c = new (std::nothrow) kvx_cache();
   if (!c) return set_error(KVX_E_STATE, "out of host memory");
   c->device = device;
@@ -336,14 +338,12 @@ int kvx_cache_create(void* pool, const kvx_block_layout* layout, int32_t format,
   c->layout = *layout;
   c->format = format;
   entry_sizes(*layout, format, &c->logical_bytes, &c->scale_offset, &c->entry_stride);
-  c->split = split_streams != 0;
+  c->save_stream = (hipStream_t)save_stream;
+  c->restore_stream = (hipStream_t)restore_stream;
+  c->split = save_stream != restore_stream;
   c->pending_save.assign(layout->num_blocks, nullptr);
   c->pending_restore.assign(layout->num_blocks, nullptr);
   rc = hip_status(hipSetDevice(device), "hipSetDevice");
-  if (!rc) rc = hip_status(hipStreamCreateWithFlags(&c->save_stream, hipStreamNonBlocking), "hipStreamCreate");
-  if (!rc && c->split)
-    rc = hip_status(hipStreamCreateWithFlags(&c->restore_stream, hipStreamNonBlocking), "hipStreamCreate");
-  if (!rc && !c->split) c->restore_stream = c->save_stream;
   if (!rc) rc = hip_status(hipEventCreateWithFlags(&c->marker, hipEventDisableTiming), "hipEventCreate");
   if (rc) {
     kvx_cache_destroy(c);
@@ -367,9 +367,7 @@ int kvx_cache_destroy(kvx_cache* c) {
     delete e;
   }
   if (c->marker) (void)hipEventDestroy(c->marker);
-  if (c->split && c->restore_stream) (void)hipStreamDestroy(c->restore_stream);
-  if (c->save_stream) (void)hipStreamDestroy(c->save_stream);
-  delete c;
+  delete c;  // the streams belong to the caller
   return rc;
 }
 

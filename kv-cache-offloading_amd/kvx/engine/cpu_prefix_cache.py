@@ -3,12 +3,13 @@
 Drop-in for CPUBlockCache of nanovllm/engine/cpu_prefix_cache.py: the same
 constructor, properties, errors, budget and slot bookkeeping, and the same
 duck-typed hooks the BlockManager calls. Data movement and its ordering run
-in libkvx (include/kvx.h): a native copy engine owns the save stream and, with
-split_streams=True, a separate restore stream; it gathers (and FP8-quantises)
-a pool block into device staging with one kernel and moves it to its pinned
-host slot with one DMA, and the reverse on restore. Per-block and per-slot
-events order save -> restore -> slot reuse against the caller's current
-stream without host synchronisation.
+in libkvx (include/kvx.h): a native copy engine queues work on a save stream
+and, with split_streams=True, a separate restore stream (torch streams, as in
+the reference); it gathers (and FP8-quantises) a pool block into device
+staging with one kernel and moves it to its pinned host slot with one DMA,
+and the reverse on restore. Per-block and per-slot events order save ->
+restore -> slot reuse against the caller's current stream without host
+synchronisation.
 
 Call from the engine-owning thread between steps (no locking), as the
 reference requires. The KV pool must be on a ROCm device: there is no
@@ -52,20 +53,24 @@ class CPUCacheFullError(MemoryError):
 
 
 class _CopyEngine:
-    """Owner of one kvx_cache handle (streams, events, slab/staging registry)."""
+    """Owner of one kvx_cache handle (events, slab/staging registry).
+
+    The engine queues work on two torch streams it borrows, at default
+    priority like the reference's (cpu_prefix_cache.py:110-113); torch keeps
+    them alive, so torch work queued on them (events, host-allocator
+    bookkeeping) never outlives its stream.
+    """
 
     def __init__(self, pool: torch.Tensor, layout, fmt: int, split: bool):
         self.layout, self.fmt = layout, fmt
         self.logical_bytes, self.scale_offset, self.entry_stride = ops.entry_layout(layout, fmt)
+        self.save_stream = torch.cuda.Stream(pool.device)
+        self.restore_stream = torch.cuda.Stream(pool.device) if split else self.save_stream
         handle = ctypes.c_void_p()
-        check(lib().kvx_cache_create(pool.data_ptr(), ctypes.byref(layout), fmt, int(split), pool.device.index,
-                                     ctypes.byref(handle)), "kvx_cache_create")
+        check(lib().kvx_cache_create(pool.data_ptr(), ctypes.byref(layout), fmt, self.save_stream.cuda_stream,
+                                     self.restore_stream.cuda_stream, pool.device.index, ctypes.byref(handle)),
+              "kvx_cache_create")
         self.handle = handle
-        save, restore = ctypes.c_void_p(), ctypes.c_void_p()
-        check(lib().kvx_cache_streams(handle, ctypes.byref(save), ctypes.byref(restore)), "kvx_cache_streams")
-        self.save_stream = torch.cuda.ExternalStream(save.value or 0, device=pool.device)
-        self.restore_stream = (self.save_stream if restore.value == save.value
-                               else torch.cuda.ExternalStream(restore.value or 0, device=pool.device))
 
     def set_staging(self, save: torch.Tensor, restore: torch.Tensor, entries: int):
         check(lib().kvx_cache_set_staging(self.handle, save.data_ptr(), restore.data_ptr(), entries), "staging")

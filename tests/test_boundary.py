@@ -83,7 +83,9 @@ def test_invalid_arguments_are_rejected_before_any_device_work():
         _lib.check(handle.kvx_save_blocks(4096, ctypes.byref(fp8_fp16), ops.FORMAT_FP8, ids, entries, 1, 0, None))
     out = ctypes.c_void_p()
     with pytest.raises(ValueError, match="aligned"):
-        _lib.check(handle.kvx_cache_create(4097, ctypes.byref(layout), ops.FORMAT_FP8, 1, 0, ctypes.byref(out)))
+        _lib.check(handle.kvx_cache_create(4097, ctypes.byref(layout), ops.FORMAT_FP8, 16, 16, 0, ctypes.byref(out)))
+    with pytest.raises(ValueError, match="non-null streams"):
+        _lib.check(handle.kvx_cache_create(4096, ctypes.byref(layout), ops.FORMAT_FP8, None, 16, 0, ctypes.byref(out)))
     assert out.value is None
     with pytest.raises(IndexError, match="sleep"):
         _lib.check(handle.kvx_sleep(None, -5))
