@@ -61,7 +61,8 @@ def test_codec_matches_golden_fixtures(gpu, hd, scale):
 @pytest.mark.parametrize("scale_dtype", [torch.float32, torch.bfloat16])
 def test_codec_matches_oracle_on_random_finite_rows(gpu, hd, scale_dtype):
     fp32 = scale_dtype == torch.float32
-    x = np.concatenate([finite_bf16_rows(4096, hd, seed=hd), student_t_rows(4096, hd, seed=hd + 1)])
+    # 8195 rows: not a multiple of any tile height, so the ragged last tile is exercised.
+    x = np.concatenate([finite_bf16_rows(4096, hd, seed=hd), student_t_rows(4099, hd, seed=hd + 1)])
     payload, s = quantize_on_device(x, scale_dtype, gpu)
     codes, scales = oracle.quantize(x, fp32)
     got_codes, got_scales = u8(payload), u8(s)
