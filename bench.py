@@ -148,8 +148,10 @@ def host_link_leg(torch, pool, layout, sources, dests, reps):
 
         both_s = timed(both)
 
-        # Ceiling: one contiguous pinned hipMemcpyAsync each way, and both at
-        # once, on the engine's two streams (the runtime torch loaded).
+        # Ceiling: contiguous pinned hipMemcpyAsync each way, and both at once
+        # on the engine's two streams (the runtime torch loaded), in 16
+        # interleaved pieces per direction (one multi-GB copy per stream does
+        # not always overlap with the other direction).
         hip = ctypes.CDLL("libamdhip64.so.7")
         hip.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
                                        ctypes.c_void_p]
@@ -158,15 +160,27 @@ def host_link_leg(torch, pool, layout, sources, dests, reps):
         host_a, host_b = slab.data_ptr(), slab.data_ptr() + n * stride
         s1, s2 = engine.save_stream.cuda_stream, engine.restore_stream.cuda_stream
 
+        piece = -(-link_bytes // 16)
+
+        def pieces():
+            return [(off, min(piece, link_bytes - off)) for off in range(0, link_bytes, piece)]
+
         def d2h():
-            assert hip.hipMemcpyAsync(host_a, flat_dev.data_ptr(), link_bytes, 2, s1) == 0
+            for off, size in pieces():
+                assert hip.hipMemcpyAsync(host_a + off, flat_dev.data_ptr() + off, size, 2, s1) == 0
 
         def h2d():
-            assert hip.hipMemcpyAsync(flat_dev2.data_ptr(), host_b, link_bytes, 1, s2) == 0
+            for off, size in pieces():
+                assert hip.hipMemcpyAsync(flat_dev2.data_ptr() + off, host_b + off, size, 1, s2) == 0
+
+        def both_ways():
+            for (off, size) in pieces():
+                assert hip.hipMemcpyAsync(host_a + off, flat_dev.data_ptr() + off, size, 2, s1) == 0
+                assert hip.hipMemcpyAsync(flat_dev2.data_ptr() + off, host_b + off, size, 1, s2) == 0
 
         ceil_d2h = timed(d2h)
         ceil_h2d = timed(h2d)
-        ceil_both = timed(lambda: (d2h(), h2d()))
+        ceil_both = timed(both_ways)
         gbs = lambda nbytes, s: nbytes / s / 1e9  # noqa: E731
         overlap = (save_s + restore_s - both_s) / min(save_s, restore_s)
         duplex = gbs(2 * link_bytes, both_s)

@@ -221,7 +221,11 @@ struct kvx_cache {
   }
 
   // Copies `count` entries between consecutive staging entries and host
-  // slots, merging runs of consecutive slots in one slab into one DMA.
+  // slots. Runs of consecutive slots in one slab are merged, then cut into
+  // pieces of at most kDmaPiece bytes: two multi-gigabyte copies queued at the
+  // same moment on the save and restore streams were measured to serialize
+  // (57 GB/s in total), while the same bytes in pieces ran full duplex (97 GB/s).
+  static constexpr size_t kDmaPiece = 64u << 20;
   int dma(bool to_host, uint8_t* staging, const int32_t* slots, int32_t count, hipStream_t s) {
     int32_t i = 0;
     while (i < count) {
@@ -231,9 +235,12 @@ struct kvx_cache {
         ++j;
       const size_t bytes = (size_t)(j - i - 1) * entry_stride + (size_t)logical_bytes_with_scales();
       uint8_t* d = staging + (int64_t)i * entry_stride;
-      hipError_t err = to_host ? hipMemcpyAsync(h0, d, bytes, hipMemcpyDeviceToHost, s)
-                               : hipMemcpyAsync(d, h0, bytes, hipMemcpyHostToDevice, s);
-      if (err != hipSuccess) return hip_status(err, to_host ? "D2H hipMemcpyAsync" : "H2D hipMemcpyAsync");
+      for (size_t off = 0; off < bytes; off += kDmaPiece) {
+        const size_t n = std::min(kDmaPiece, bytes - off);
+        hipError_t err = to_host ? hipMemcpyAsync(h0 + off, d + off, n, hipMemcpyDeviceToHost, s)
+                                 : hipMemcpyAsync(d + off, h0 + off, n, hipMemcpyHostToDevice, s);
+        if (err != hipSuccess) return hip_status(err, to_host ? "D2H hipMemcpyAsync" : "H2D hipMemcpyAsync");
+      }
       i = j;
     }
     return KVX_OK;

@@ -89,3 +89,177 @@ def block_selection(num_blocks: int, count: int, seed: int, exclude=()) -> list[
     if count > len(order):
         raise ValueError(f"cannot pick {count} of {len(order)} blocks")
     return order[:count]
+
+
+# ---------------------------------------------------------------------------
+# Model-free engine runs
+
+def synthetic_kv(tokens: torch.Tensor, positions: torch.Tensor, layer: int, kv: int, heads: int, head_dim: int,
+                 dtype=torch.bfloat16) -> torch.Tensor:
+    """Deterministic K (kv=0) or V (kv=1) rows [n, heads, head_dim] for tokens at positions.
+
+    A stand-in for a model's projections: any block's expected contents can be
+    recomputed from its tokens and positions alone.
+    """
+    t = tokens.to(torch.float32)[:, None, None]
+    p = positions.to(torch.float32)[:, None, None]
+    h = torch.arange(heads, device=tokens.device, dtype=torch.float32)[None, :, None]
+    d = torch.arange(head_dim, device=tokens.device, dtype=torch.float32)[None, None, :]
+    phase = 0.37 * t + 0.0113 * p + 0.71 * h + 0.173 * d + 1.31 * layer + 2.9 * kv
+    amp = 1.0 + 4.0 * (((d.to(torch.int64) * 7 + h.to(torch.int64) * 3 + layer) % 29) == 0)  # outlier channels
+    return (torch.sin(phase) * amp).to(dtype)
+
+
+class SyntheticKVRunner:
+    """Runner for kvx.engine.llm_engine.LLMEngine that writes every scheduled token's K/V.
+
+    call("run", seqs, is_prefill) computes the slot mapping the way
+    nanovllm's ModelRunner does (model_runner.py:156-166, 186), writes
+    synthetic_kv rows for all layers through kvx.ops.store_kvcache on the
+    current stream and returns `next_token` for each sequence.
+    """
+
+    def __init__(self, pool: torch.Tensor, next_token: int = 1):
+        self.kv_cache = pool
+        self.world_size = 1
+        self.block_size = pool.shape[3]
+        self.next_token = next_token
+        self.tokens_written = 0
+
+    def call(self, method, *args):
+        if method == "exit":
+            return None
+        from kvx import ops
+        from kvx.engine.llm_engine import decode_slot_mapping, prefill_slot_mapping
+
+        seqs, is_prefill = args
+        bs = self.block_size
+        if is_prefill:
+            slots = prefill_slot_mapping(seqs, bs)
+            toks, pos = [], []
+            for seq in seqs:
+                start = seq.num_cached_tokens
+                toks += seq.token_ids[start:start + seq.num_scheduled_tokens]
+                pos += range(start, start + seq.num_scheduled_tokens)
+        else:
+            slots = decode_slot_mapping(seqs, bs)
+            toks = [seq.last_token for seq in seqs]
+            pos = [len(seq) - 1 for seq in seqs]
+        if slots:
+            pool = self.kv_cache
+            dev = pool.device
+            t = torch.tensor(toks, device=dev)
+            p = torch.tensor(pos, device=dev)
+            mapping = torch.tensor(slots, dtype=torch.int32, device=dev)
+            heads, hd = pool.shape[4], pool.shape[5]
+            for layer in range(pool.shape[1]):
+                k = synthetic_kv(t, p, layer, 0, heads, hd, pool.dtype)
+                v = synthetic_kv(t, p, layer, 1, heads, hd, pool.dtype)
+                ops.store_kvcache(k, v, pool[0, layer], pool[1, layer], mapping)
+            self.tokens_written += len(slots)
+        return [self.next_token] * len(seqs)
+
+
+def expected_block(pool: torch.Tensor, token_ids, start_position: int) -> torch.Tensor:
+    """[2, L, BS, H, hd] contents SyntheticKVRunner writes for one full block of tokens."""
+    dev = pool.device
+    t = torch.tensor(list(token_ids), device=dev)
+    p = torch.arange(start_position, start_position + len(token_ids), device=dev)
+    heads, hd = pool.shape[4], pool.shape[5]
+    return torch.stack([torch.stack([synthetic_kv(t, p, layer, kv, heads, hd, pool.dtype)
+                                     for layer in range(pool.shape[1])]) for kv in range(2)])
+
+
+@dataclass
+class AgentPressureResult:
+    turns: int
+    wall_s: float
+    saved_blocks: int
+    restored_blocks: int
+    prefetched_blocks: int
+    budget_skips: int
+    d2h_bytes: int
+    h2d_bytes: int
+    blocks_checked: int
+    blocks_fp8_round_trip: int
+
+    @property
+    def link_gbs(self) -> float:
+        return (self.d2h_bytes + self.h2d_bytes) / self.wall_s / 1e9
+
+
+def run_agent_pressure(engine, agents: int = 4, context: int = 32768, turns: int = 12, append: int = 2048,
+                       seed: int = 0, verify: bool = True, verify_stride: int = 1,
+                       prefetch_hints: bool = True) -> AgentPressureResult:
+    """Multi-turn agents sharing one pool: each turn an agent returns with its whole context plus `append`
+    new tokens, evicting others' blocks (saved to the CPU tier) and restoring or prefetching its own.
+
+    With verify=True every `verify_stride`-th full block (and the last) of each finished request must hold
+    either the exact synthetic KV (GPU hit or recomputed) or its FP8 round trip (restored from an FP8 entry) --
+    a block restored from the wrong slot, or read before its restore finished, matches neither. Before each
+    request the next agent's prefix is hinted with prefetch_prefix, so its restores (H2D) overlap the saves
+    (D2H) of the blocks the current request evicts.
+    """
+    import time
+
+    from kvx import ops
+    from kvx.engine.sequence import SamplingParams, Sequence
+
+    g = torch.Generator().manual_seed(seed)
+    histories = [torch.randint(2, 50000, (context,), generator=g).tolist() for _ in range(agents)]
+    pool = engine.model_runner.kv_cache
+    cache = engine._cpu_prefix_cache
+    bs = pool.shape[3]
+    params = SamplingParams(temperature=0, max_tokens=1, ignore_eos=True)
+    checked = fp8_hits = 0
+    t0 = time.perf_counter()
+    for turn in range(turns):
+        for a in range(agents):
+            histories[a] += torch.randint(2, 50000, (append,), generator=g).tolist()
+            if prefetch_hints and agents > 1:
+                nxt = (a + 1) % agents
+                engine.prefetch_prefix(Sequence(histories[nxt]))
+            seq_id = engine.add_request(histories[a], params)
+            seq = next(s for s in engine.scheduler.waiting if s.seq_id == seq_id)
+            while not engine.is_finished():
+                engine.step()
+            histories[a] += [engine.model_runner.next_token]
+            if verify:
+                # The request's full blocks are now idle GPU hits: check a sample of them.
+                manager = engine.scheduler.block_manager
+                h = -1
+                full_blocks = (len(histories[a]) - 1) // bs
+                for i in range(full_blocks):
+                    tokens = histories[a][i * bs:(i + 1) * bs]
+                    h = manager.compute_hash(tokens, h)
+                    block_id = manager.hash_to_block_id.get(h)
+                    if block_id is None:
+                        break
+                    if i % verify_stride and i != full_blocks - 1:
+                        continue
+                    if cache is not None:
+                        cache.before_block_use(block_id)
+                    expect = expected_block(pool, tokens, i * bs)
+                    got = pool[:, :, block_id]
+                    if torch.equal(got.view(torch.int16), expect.view(torch.int16)):
+                        checked += 1
+                        continue
+                    payload = torch.empty(expect.shape, dtype=torch.float8_e4m3fn, device=pool.device)
+                    scale = torch.empty((*expect.shape[:-1], 1), dtype=cache._scale_dtype, device=pool.device)
+                    ops.fp8_quantize(expect, payload, scale)
+                    round_trip = torch.empty_like(expect)
+                    ops.fp8_dequantize(payload, scale, round_trip)
+                    if not torch.equal(got.view(torch.int16), round_trip.view(torch.int16)):
+                        raise AssertionError(f"turn {turn} agent {a}: block {i} (GPU block {block_id}) holds "
+                                             "neither its KV nor the FP8 round trip of it")
+                    checked += 1
+                    fp8_hits += 1
+    if cache is not None:
+        cache.synchronize()
+    torch.cuda.synchronize(pool.device)
+    wall = time.perf_counter() - t0
+    stats = cache.stats if cache is not None else {"saved_blocks": 0, "restored_blocks": 0, "budget_skips": 0}
+    entry = cache.block_bytes if cache is not None else 0
+    return AgentPressureResult(turns * agents, wall, stats["saved_blocks"], stats["restored_blocks"],
+                               cache.prefetched_blocks if cache is not None else 0, stats["budget_skips"],
+                               stats["saved_blocks"] * entry, stats["restored_blocks"] * entry, checked, fp8_hits)

@@ -1,0 +1,25 @@
+"""Config 5: agent pressure on the Qwen3-8B pool through the whole engine (store_kvcache, FP8 saves,
+restores and prefetches on split streams under slot reuse), verified block by block."""
+
+import pytest
+import torch
+
+from kvx.engine.llm_engine import LLMEngine
+from kvx.workloads import QWEN3_8B, SyntheticKVRunner, run_agent_pressure
+
+pytestmark = pytest.mark.gpu
+
+
+def test_config5_agent_pressure_restores_the_right_bytes(gpu):
+    pool = torch.zeros(QWEN3_8B.shape, dtype=torch.bfloat16, device=gpu)
+    engine = LLMEngine(SyntheticKVRunner(pool), max_num_batched_tokens=16384, max_num_seqs=4, eos=-1,
+                       kvcache_block_size=256, num_kvcache_blocks=QWEN3_8B.num_blocks)
+    cache = engine.create_cpu_prefix_cache(8 << 30, automatic=True, prefetch=True, split_streams=True, fp8=True,
+                                           scale_dtype=torch.float32)
+    result = run_agent_pressure(engine, agents=4, context=32768, turns=12, append=2048, verify=True,
+                                verify_stride=8)
+    print(result, f"{result.link_gbs:.1f} GB/s over the run")
+    assert result.saved_blocks > 0 and result.restored_blocks > 0 and result.prefetched_blocks > 0
+    assert result.blocks_fp8_round_trip > 0 and result.blocks_checked > result.blocks_fp8_round_trip
+    engine.exit()
+    assert cache.closed
