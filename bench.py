@@ -50,6 +50,7 @@ def parse_args():
     p.add_argument("--scale", choices=("fp32", "bf16"), default="fp32")
     p.add_argument("--skip-host-link", action="store_true")
     p.add_argument("--skip-cpu-baseline", action="store_true")
+    p.add_argument("--skip-store", action="store_true", help="skip the store_kvcache leg")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample budget")
     p.add_argument("--host-reps", type=int, default=3)
     p.add_argument("--calibrate-copy", action="store_true",
@@ -103,6 +104,51 @@ def kernel_leg(torch, ops, pool, sources, dests, scale_dtype, steps, warmup):
     hbm_bytes = n * (BF16_BLOCK_BYTES + logical)  # per launch, either direction
     return dict(elapsed=elapsed, save_ms=save_ms, restore_ms=restore_ms, hbm_bytes=hbm_bytes,
                 logical_entry=logical, entry_stride=stride)
+
+
+def store_leg(torch, ops, pool, reps=5):
+    """store_kvcache over all layers for a ragged batch of 16 sequences (lengths U[1, 8192], seeded).
+
+    K is contiguous; V is a strided view of a fused QKV output (row stride
+    (32 + 2H) * hd, as Qwen3-8B's). Slots are distinct random pool slots;
+    the batch is padded to a multiple of 256 with -1 slots.
+    """
+    import numpy as np
+
+    _, layers, nb, bs, heads, hd = pool.shape
+    rng = np.random.default_rng(7)
+    lengths = rng.integers(1, 8193, size=16)
+    total = int(min(lengths.sum(), nb * bs))
+    padded = -(-total // 256) * 256
+    slots = np.full(padded, -1, dtype=np.int32)
+    slots[:total] = rng.permutation(nb * bs)[:total]
+    g = torch.Generator(device=pool.device).manual_seed(8)
+    qkv = torch.randn((padded, (32 + 2 * heads) * hd), generator=g, device=pool.device).to(torch.bfloat16)
+    key = qkv[:, 32 * hd:(32 + heads) * hd].contiguous().view(padded, heads, hd)
+    value = qkv[:, (32 + heads) * hd:].view(padded, heads, hd)
+    mapping = torch.from_numpy(slots).to(pool.device)
+    stream = torch.cuda.current_stream(pool.device)
+
+    def run():
+        for layer in range(layers):
+            ops.store_kvcache(key, value, pool[0, layer], pool[1, layer], mapping)
+
+    run()
+    times = []
+    for _ in range(reps):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        run()
+        end.record(stream)
+        end.synchronize()
+        times.append(start.elapsed_time(end) / 1000)
+    t = sorted(times)[len(times) // 2]
+    row = heads * hd * 2
+    per_launch = total * 4 * row + padded * 4  # K and V rows read and written, plus the slot map
+    gbs = layers * per_launch / t / 1e9
+    return {"tokens": total, "padded_tokens": padded, "layers": layers, "ms_all_layers": round(1000 * t, 4),
+            "algorithmic_bytes_per_launch": per_launch, "hbm_gbs": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 def host_link_leg(torch, pool, layout, sources, dests, reps):
@@ -316,6 +362,9 @@ def main():
             "algorithmic_bytes_per_launch": k["hbm_bytes"],
         },
     }
+    if not args.skip_store:
+        log("store_kvcache leg")
+        result["store_kvcache"] = store_leg(torch, ops, pool)
     if args.calibrate_copy:
         raw_layout = ops.pool_layout(pool)
         _, _, raw_stride = ops.entry_layout(raw_layout, ops.FORMAT_RAW)

@@ -126,6 +126,21 @@ int kvx_restore_blocks(void* pool, const kvx_block_layout* layout, int32_t forma
                        int64_t scale_offset, void* stream);
 
 /*
+ * Token-granular KV handoff copies (nanovllm/engine/kv_handoff.py). A
+ * sequence's first num_rows (token, head) rows live in the pool blocks
+ * block_table_host[0..]; the dense buffer holds them as
+ * [planes][num_rows][head_dim] (the reference's [2, L, tokens, H, hd] payload,
+ * num_rows = tokens * H). Byte copies; any element size in `layout`.
+ * kvx_gather_tokens replaces export_kv's index_select + contiguous
+ * (:46-55); kvx_scatter_tokens replaces import_kv's per-block copy_
+ * (:112-118). The buffer may be device memory or mapped pinned host memory.
+ */
+int kvx_gather_tokens(const void* pool, const kvx_block_layout* layout, const int32_t* block_table_host,
+                      int32_t table_len, int64_t num_rows, void* dst, void* stream);
+int kvx_scatter_tokens(void* pool, const kvx_block_layout* layout, const int32_t* block_table_host,
+                       int32_t table_len, int64_t num_rows, const void* src, void* stream);
+
+/*
  * Copy engine: the stream/event half of CPUBlockCache
  * (nanovllm/engine/cpu_prefix_cache.py:72-131, 270-273, 306-322, 352-363,
  * 370-398). It queues copies on a save stream and a restore stream that the
@@ -186,6 +201,22 @@ int kvx_cache_synchronize(kvx_cache* cache);
 /* Counts of engine activity: saves, restores, waits inserted; for tests and stats. */
 int kvx_cache_counters(kvx_cache* cache, int64_t* saved_blocks, int64_t* restored_blocks,
                        int64_t* stream_waits);
+
+/*
+ * Negative controls (tests only): each flag drops one ordering rule so a test
+ * can show that its check fails without it (the reference claims such controls,
+ * README.md:114-117, but commits none). Flags:
+ *   KVX_DEBUG_SKIP_SAVE_WAIT       a restore does not wait for its slot's save
+ *   KVX_DEBUG_SKIP_SLOT_READ_WAIT  a save does not wait for restores reading its slot
+ *   KVX_DEBUG_SKIP_REUSE_WAIT      before_block_reuse does not wait for the block's save
+ *   KVX_DEBUG_SKIP_VICTIM_WAIT     a restore does not wait for a pending save of its destination
+ * Results are wrong (never a fault) while a flag is set; 0 restores normal operation.
+ */
+#define KVX_DEBUG_SKIP_SAVE_WAIT 1
+#define KVX_DEBUG_SKIP_SLOT_READ_WAIT 2
+#define KVX_DEBUG_SKIP_REUSE_WAIT 4
+#define KVX_DEBUG_SKIP_VICTIM_WAIT 8
+int kvx_cache_set_debug(kvx_cache* cache, int32_t flags);
 
 /*
  * Queues a kernel that keeps one wave busy for `microseconds` on `stream`

@@ -110,6 +110,41 @@ static int run_batches(bool save, void* pool, const kvx_block_layout* layout, in
   return KVX_OK;
 }
 
+// Token-granular copy between the blocks in `table` and a dense buffer.
+static int token_copy(bool gather, void* pool, const kvx_block_layout* l, const int32_t* table, int32_t table_len,
+                      int64_t num_rows, void* dense, hipStream_t stream) {
+  int rc = check_layout(l, KVX_FORMAT_RAW);
+  if (rc) return rc;
+  if (num_rows < 0 || table_len < 0) return set_error(KVX_E_INVALID, "negative row or block count");
+  if (num_rows == 0) return KVX_OK;
+  if (!pool || !dense || !table) return set_error(KVX_E_INVALID, "NULL pool, buffer or block table");
+  if ((uintptr_t)pool % 2 || (uintptr_t)dense % 2) return set_error(KVX_E_INVALID, "buffers must be 2-byte aligned");
+  const int64_t row_bytes = (int64_t)l->head_dim * l->elem_bytes;
+  const int64_t plane_bytes = (int64_t)l->plane_rows * row_bytes;
+  const int64_t nblocks = (num_rows + l->plane_rows - 1) / l->plane_rows;
+  if (nblocks > table_len)
+    return set_error(KVX_E_RANGE, "%lld rows need %lld blocks, the table has %d", (long long)num_rows,
+                     (long long)nblocks, table_len);
+  for (int64_t i = 0; i < nblocks; ++i)
+    if (table[i] < 0 || table[i] >= l->num_blocks)
+      return set_error(KVX_E_RANGE, "block id %d outside [0, %d)", table[i], l->num_blocks);
+  const int64_t dense_plane_stride = num_rows * row_bytes;
+  const int64_t tail_bytes = (num_rows - (nblocks - 1) * l->plane_rows) * row_bytes;
+  BlockBatch b;
+  for (int64_t base = 0; base < nblocks; base += kMaxBatch) {
+    b.n = (int32_t)std::min<int64_t>(kMaxBatch, nblocks - base);
+    for (int32_t i = 0; i < b.n; ++i) {
+      b.ids[i] = table[base + i];
+      b.entries[i] = (uint64_t)(uintptr_t)dense + (uint64_t)((base + i) * plane_bytes);
+    }
+    const int64_t last = base + b.n == nblocks ? tail_bytes : plane_bytes;
+    const bool vec = vector_access_ok(pool, *l, b.entries, b.n);
+    hipError_t err = launch_token_copy(gather, pool, *l, b, vec, dense_plane_stride, last, stream);
+    if (err != hipSuccess) return hip_status(err, gather ? "token gather launch" : "token scatter launch");
+  }
+  return KVX_OK;
+}
+
 }  // namespace kvx
 
 using namespace kvx;
@@ -150,6 +185,7 @@ struct kvx_cache {
   std::vector<Event*> slot_read, slot_saved;          // per host slot
   std::vector<Event*> free_events, all_events;
   int64_t saved = 0, restored = 0, waits = 0;
+  int32_t debug = 0;  // KVX_DEBUG_* negative-control flags
 
   uint8_t* host_entry(int32_t slot) const {
     for (const Slab& s : slabs)
@@ -318,6 +354,18 @@ int kvx_restore_blocks(void* pool, const kvx_block_layout* layout, int32_t forma
                      (hipStream_t)stream);
 }
 
+int kvx_gather_tokens(const void* pool, const kvx_block_layout* layout, const int32_t* block_table_host,
+                      int32_t table_len, int64_t num_rows, void* dst, void* stream) {
+  return token_copy(true, const_cast<void*>(pool), layout, block_table_host, table_len, num_rows, dst,
+                    (hipStream_t)stream);
+}
+
+int kvx_scatter_tokens(void* pool, const kvx_block_layout* layout, const int32_t* block_table_host,
+                       int32_t table_len, int64_t num_rows, const void* src, void* stream) {
+  return token_copy(false, pool, layout, block_table_host, table_len, num_rows, const_cast<void*>(src),
+                    (hipStream_t)stream);
+}
+
 int kvx_sleep(void* stream, int64_t microseconds) {
   if (microseconds < 0 || microseconds > 60LL * 1000 * 1000)
     return set_error(KVX_E_RANGE, "sleep must be within [0, 60 s]");
@@ -435,7 +483,7 @@ int kvx_cache_save(kvx_cache* c, const int32_t* ids, const int32_t* slots, int32
   rc = c->wait_stream(s, (hipStream_t)compute_stream);
   if (rc) return rc;
   // With split streams, after the last restore that read each target slot (:312-314).
-  if (c->split) {
+  if (c->split && !(c->debug & KVX_DEBUG_SKIP_SLOT_READ_WAIT)) {
     for (int32_t i = 0; i < n; ++i) {
       Event*& r = c->slot_read[slots[i]];
       if (r) {
@@ -482,13 +530,13 @@ int kvx_cache_restore(kvx_cache* c, const int32_t* slots, const int32_t* ids, in
   if (c->split) {
     for (int32_t i = 0; i < n; ++i) {
       // The payload may still be arriving from its own save (:380-381).
-      Event* sv = c->slot_saved[slots[i]];
+      Event* sv = (c->debug & KVX_DEBUG_SKIP_SAVE_WAIT) ? nullptr : c->slot_saved[slots[i]];
       if (sv) {
         rc = c->wait_event(s, sv);
         if (rc) return rc;
       }
       // A save of the destination's previous contents may still be reading it.
-      Event* ps = c->pending_save[ids[i]];
+      Event* ps = (c->debug & KVX_DEBUG_SKIP_VICTIM_WAIT) ? nullptr : c->pending_save[ids[i]];
       if (ps && ps != sv) {
         rc = c->wait_event(s, ps);
         if (rc) return rc;
@@ -525,6 +573,10 @@ int kvx_cache_before_block_reuse(kvx_cache* c, int32_t block_id, void* compute_s
     return set_error(KVX_E_RANGE, "block id %d outside [0, %d)", block_id, c->layout.num_blocks);
   for (std::vector<Event*>* pending : {&c->pending_save, &c->pending_restore}) {
     Event*& e = (*pending)[block_id];
+    if (e && pending == &c->pending_save && (c->debug & KVX_DEBUG_SKIP_REUSE_WAIT)) {
+      c->unref(e);
+      continue;
+    }
     if (e) {
       int rc = c->wait_event((hipStream_t)compute_stream, e);
       if (rc) return rc;
@@ -544,6 +596,15 @@ int kvx_cache_before_block_use(kvx_cache* c, int32_t block_id, void* compute_str
     if (rc) return rc;
     c->unref(e);
   }
+  return KVX_OK;
+}
+
+int kvx_cache_set_debug(kvx_cache* c, int32_t flags) {
+  if (!c) return set_error(KVX_E_INVALID, "NULL cache");
+  if (flags & ~(KVX_DEBUG_SKIP_SAVE_WAIT | KVX_DEBUG_SKIP_SLOT_READ_WAIT | KVX_DEBUG_SKIP_REUSE_WAIT |
+                KVX_DEBUG_SKIP_VICTIM_WAIT))
+    return set_error(KVX_E_INVALID, "unknown debug flags %d", flags);
+  c->debug = flags;
   return KVX_OK;
 }
 

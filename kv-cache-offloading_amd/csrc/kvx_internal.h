@@ -44,6 +44,12 @@ hipError_t launch_save(const void* pool, const kvx_block_layout& layout, int32_t
                        const BlockBatch& batch, int64_t scale_offset, bool vector_ok, hipStream_t stream);
 hipError_t launch_restore(void* pool, const kvx_block_layout& layout, int32_t format,
                           const BlockBatch& batch, int64_t scale_offset, bool vector_ok, hipStream_t stream);
+// Token gather/scatter between a sequence's blocks and a dense
+// [planes][rows][head_dim] buffer: entries are the dense buffer at
+// block_index * plane_bytes, dense_plane_stride apart per plane, and the
+// batch's last block copies last_bytes per plane.
+hipError_t launch_token_copy(bool gather, void* pool, const kvx_block_layout& layout, const BlockBatch& batch,
+                             bool vector_ok, int64_t dense_plane_stride, int64_t last_bytes, hipStream_t stream);
 // True when 16-byte vector kernels may address this pool/entry combination.
 bool vector_access_ok(const void* pool, const kvx_block_layout& layout, const uint64_t* entries, int32_t n);
 hipError_t launch_store_kvcache(const void* key, int64_t key_stride, const void* value,

@@ -421,10 +421,14 @@ __global__ __launch_bounds__(kThreads) void fp8_restore_generic(uint16_t* __rest
 
 constexpr int kCopyVecs = 4;  // uint4 per thread per tile: 16 KiB tiles
 
+// Entry e receives plane p of its block at entries[e] + p * entry_plane_stride;
+// every entry copies plane_bytes per plane except the batch's last, which
+// copies last_bytes (a sequence's partial final block in a token gather).
 template <bool kToEntry>
 __global__ __launch_bounds__(kThreads) void raw_copy_kernel(uint8_t* __restrict__ pool, PlaneGeom g,
                                                            BlockBatch b, int64_t plane_bytes,
-                                                           int64_t elem_bytes) {
+                                                           int64_t elem_bytes, int64_t entry_plane_stride,
+                                                           int64_t last_bytes) {
   constexpr int kTileBytes = kThreads * kCopyVecs * 16;
   const int per_entry = g.planes * g.chunks;
   const int tile = xcd_tile(blockIdx.x, gridDim.x);
@@ -432,28 +436,30 @@ __global__ __launch_bounds__(kThreads) void raw_copy_kernel(uint8_t* __restrict_
   const int rem = tile - e * per_entry;
   const int p = rem / g.chunks;
   const int64_t off0 = (int64_t)(rem - p * g.chunks) * kTileBytes;
+  const int64_t valid = e == b.n - 1 ? last_bytes : plane_bytes;
   uint8_t* pl = pool + ((int64_t)b.ids[e] * g.block_stride + (int64_t)p * g.plane_stride) * elem_bytes;
-  uint8_t* en = reinterpret_cast<uint8_t*>(b.entries[e]) + (int64_t)p * plane_bytes;
+  uint8_t* en = reinterpret_cast<uint8_t*>(b.entries[e]) + (int64_t)p * entry_plane_stride;
   const uint8_t* src = kToEntry ? pl : en;
   uint8_t* dst = kToEntry ? en : pl;
   uint4 v[kCopyVecs];
 #pragma unroll
   for (int k = 0; k < kCopyVecs; ++k) {
     const int64_t off = off0 + ((int64_t)k * kThreads + threadIdx.x) * 16;
-    v[k] = off < plane_bytes ? *reinterpret_cast<const uint4*>(src + off) : make_uint4(0, 0, 0, 0);
+    v[k] = off < valid ? *reinterpret_cast<const uint4*>(src + off) : make_uint4(0, 0, 0, 0);
   }
 #pragma unroll
   for (int k = 0; k < kCopyVecs; ++k) {
     const int64_t off = off0 + ((int64_t)k * kThreads + threadIdx.x) * 16;
-    if (off < plane_bytes) store_nt16(dst + off, v[k]);
+    if (off < valid) store_nt16(dst + off, v[k]);
   }
 }
 
-// Plane sizes that are not a multiple of 16 bytes: 2-byte granules.
+// Sizes or strides that are not multiples of 16 bytes: 2-byte granules.
 template <bool kToEntry>
 __global__ __launch_bounds__(kThreads) void raw_copy_generic(uint8_t* __restrict__ pool, PlaneGeom g,
                                                             BlockBatch b, int64_t plane_bytes,
-                                                            int64_t elem_bytes) {
+                                                            int64_t elem_bytes, int64_t entry_plane_stride,
+                                                            int64_t last_bytes) {
   const int64_t granules = plane_bytes / 2;
   const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   const int64_t per_entry = granules * g.planes;
@@ -462,8 +468,9 @@ __global__ __launch_bounds__(kThreads) void raw_copy_generic(uint8_t* __restrict
   const int64_t rem = idx - e * per_entry;
   const int64_t p = rem / granules;
   const int64_t k = rem - p * granules;
+  if (e == b.n - 1 && k >= last_bytes / 2) return;
   uint16_t* pl = reinterpret_cast<uint16_t*>(pool + ((int64_t)b.ids[e] * g.block_stride + p * g.plane_stride) * elem_bytes);
-  uint16_t* en = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(b.entries[e]) + p * plane_bytes);
+  uint16_t* en = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(b.entries[e]) + p * entry_plane_stride);
   if (kToEntry) en[k] = pl[k];
   else pl[k] = en[k];
 }
@@ -662,30 +669,40 @@ static hipError_t launch_fp8(bool save, void* pool, const kvx_block_layout& l, c
 }
 
 static hipError_t launch_raw(bool to_entry, void* pool, const kvx_block_layout& l, const BlockBatch& b,
-                             bool vector_ok, hipStream_t stream) {
+                             bool vector_ok, int64_t entry_plane_stride, int64_t last_bytes, hipStream_t stream) {
   const int64_t plane_bytes = (int64_t)l.plane_rows * l.head_dim * l.elem_bytes;
-  if (vector_ok && plane_bytes % 16 == 0) {
+  if (entry_plane_stride < 0) entry_plane_stride = plane_bytes;
+  if (last_bytes < 0) last_bytes = plane_bytes;
+  const bool vec = vector_ok && plane_bytes % 16 == 0 && entry_plane_stride % 16 == 0 && last_bytes % 16 == 0;
+  const int64_t es = l.elem_bytes;
+  if (vec) {
     constexpr int kTileBytes = kThreads * kCopyVecs * 16;
     PlaneGeom g = make_geom(l, 0, 0);
     g.chunks = (int32_t)((plane_bytes + kTileBytes - 1) / kTileBytes);
     const unsigned grid = (unsigned)(b.n * g.planes * g.chunks);
     if (to_entry)
       hipLaunchKernelGGL(raw_copy_kernel<true>, dim3(grid), dim3(kThreads), 0, stream, (uint8_t*)pool, g, b,
-                         plane_bytes, (int64_t)l.elem_bytes);
+                         plane_bytes, es, entry_plane_stride, last_bytes);
     else
       hipLaunchKernelGGL(raw_copy_kernel<false>, dim3(grid), dim3(kThreads), 0, stream, (uint8_t*)pool, g, b,
-                         plane_bytes, (int64_t)l.elem_bytes);
+                         plane_bytes, es, entry_plane_stride, last_bytes);
   } else {
     PlaneGeom g = make_geom(l, 0, 0);
     const unsigned grid = generic_grid((int64_t)b.n * l.planes * (plane_bytes / 2));
     if (to_entry)
       hipLaunchKernelGGL(raw_copy_generic<true>, dim3(grid), dim3(kThreads), 0, stream, (uint8_t*)pool, g, b,
-                         plane_bytes, (int64_t)l.elem_bytes);
+                         plane_bytes, es, entry_plane_stride, last_bytes);
     else
       hipLaunchKernelGGL(raw_copy_generic<false>, dim3(grid), dim3(kThreads), 0, stream, (uint8_t*)pool, g, b,
-                         plane_bytes, (int64_t)l.elem_bytes);
+                         plane_bytes, es, entry_plane_stride, last_bytes);
   }
   return hipGetLastError();
+}
+
+hipError_t launch_token_copy(bool gather, void* pool, const kvx_block_layout& l, const BlockBatch& b,
+                             bool vector_ok, int64_t dense_plane_stride, int64_t last_bytes, hipStream_t stream) {
+  if (b.n <= 0) return hipSuccess;
+  return launch_raw(gather, pool, l, b, vector_ok, dense_plane_stride, last_bytes, stream);
 }
 
 bool vector_access_ok(const void* pool, const kvx_block_layout& l, const uint64_t* entries, int32_t n) {
@@ -700,7 +717,7 @@ hipError_t launch_save(const void* pool, const kvx_block_layout& l, int32_t form
                        int64_t scale_offset, bool vector_ok, hipStream_t stream) {
   if (b.n <= 0) return hipSuccess;
   void* p = const_cast<void*>(pool);
-  if (format == KVX_FORMAT_RAW) return launch_raw(true, p, l, b, vector_ok, stream);
+  if (format == KVX_FORMAT_RAW) return launch_raw(true, p, l, b, vector_ok, -1, -1, stream);
   return l.scale_dtype == KVX_SCALE_BF16 ? launch_fp8<true>(true, p, l, b, scale_offset, vector_ok, stream)
                                          : launch_fp8<false>(true, p, l, b, scale_offset, vector_ok, stream);
 }
@@ -708,7 +725,7 @@ hipError_t launch_save(const void* pool, const kvx_block_layout& l, int32_t form
 hipError_t launch_restore(void* pool, const kvx_block_layout& l, int32_t format, const BlockBatch& b,
                           int64_t scale_offset, bool vector_ok, hipStream_t stream) {
   if (b.n <= 0) return hipSuccess;
-  if (format == KVX_FORMAT_RAW) return launch_raw(false, pool, l, b, vector_ok, stream);
+  if (format == KVX_FORMAT_RAW) return launch_raw(false, pool, l, b, vector_ok, -1, -1, stream);
   return l.scale_dtype == KVX_SCALE_BF16 ? launch_fp8<true>(false, pool, l, b, scale_offset, vector_ok, stream)
                                          : launch_fp8<false>(false, pool, l, b, scale_offset, vector_ok, stream);
 }

@@ -19,6 +19,7 @@ ABI_VERSION = 1
 E_INVALID, E_RANGE, E_STATE, E_UNSUPPORTED = -1, -2, -3, -4
 SCALE_BF16, SCALE_FP32 = 0, 1
 FORMAT_RAW, FORMAT_FP8 = 0, 1
+DEBUG_SKIP_SAVE_WAIT, DEBUG_SKIP_SLOT_READ_WAIT, DEBUG_SKIP_REUSE_WAIT, DEBUG_SKIP_VICTIM_WAIT = 1, 2, 4, 8
 
 _c_p = ctypes.c_void_p
 _i32, _i64 = ctypes.c_int32, ctypes.c_int64
@@ -53,6 +54,8 @@ SIGNATURES = {
                                ctypes.POINTER(ctypes.c_uint64), _i32, _i64, _c_p]),
     "kvx_restore_blocks": (_i32, [_c_p, ctypes.POINTER(BlockLayout), _i32, ctypes.POINTER(_i32),
                                   ctypes.POINTER(ctypes.c_uint64), _i32, _i64, _c_p]),
+    "kvx_gather_tokens": (_i32, [_c_p, ctypes.POINTER(BlockLayout), ctypes.POINTER(_i32), _i32, _i64, _c_p, _c_p]),
+    "kvx_scatter_tokens": (_i32, [_c_p, ctypes.POINTER(BlockLayout), ctypes.POINTER(_i32), _i32, _i64, _c_p, _c_p]),
     "kvx_cache_create": (_i32, [_c_p, ctypes.POINTER(BlockLayout), _i32, _c_p, _c_p, _i32, ctypes.POINTER(_c_p)]),
     "kvx_cache_destroy": (_i32, [_c_p]),
     "kvx_cache_set_staging": (_i32, [_c_p, _c_p, _c_p, _i32]),
@@ -65,6 +68,7 @@ SIGNATURES = {
     "kvx_cache_before_block_use": (_i32, [_c_p, _i32, _c_p]),
     "kvx_cache_synchronize": (_i32, [_c_p]),
     "kvx_cache_counters": (_i32, [_c_p, ctypes.POINTER(_i64), ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
+    "kvx_cache_set_debug": (_i32, [_c_p, _i32]),
     "kvx_sleep": (_i32, [_c_p, _i64]),
     "kvx_selftest": (_i32, [_c_p, _c_p]),
 }

@@ -100,6 +100,10 @@ class _CopyEngine:
         check(lib().kvx_cache_counters(self.handle, *map(ctypes.byref, vals)), "kvx_cache_counters")
         return dict(zip(("saved_blocks", "restored_blocks", "stream_waits"), (v.value for v in vals)))
 
+    def set_debug(self, flags: int):
+        """Negative controls for tests: drop ordering rules (kvx._lib.DEBUG_*); results become wrong."""
+        check(lib().kvx_cache_set_debug(self.handle, flags), "kvx_cache_set_debug")
+
     def reset_slabs(self):
         check(lib().kvx_cache_reset_slabs(self.handle), "kvx_cache_reset_slabs")
 

@@ -1,0 +1,107 @@
+"""Uncompressed KV handoff of a running request between engines (TP=1).
+
+Same snapshot format and semantics as nanovllm/engine/kv_handoff.py: the
+payload holds the written tokens only, in logical order, on the CPU, as
+[K/V, layer, token, KV head, head dim]. The gather (export) and scatter
+(import) run as libkvx token-copy kernels instead of index_select + per-block
+copy_; the host copies are torch's.
+"""
+
+from dataclasses import dataclass
+
+import torch
+
+from kvx import ops
+from kvx.engine.sequence import SamplingParams, Sequence, SequenceStatus
+
+
+@dataclass
+class KVSnapshot:
+    token_ids: list[int]
+    num_prompt_tokens: int
+    num_cached_tokens: int
+    block_size: int
+    temperature: float
+    max_tokens: int
+    ignore_eos: bool
+    kv: torch.Tensor  # [K/V, layer, written token, KV head, head dim], CPU
+
+    @property
+    def payload_bytes(self):
+        return self.kv.numel() * self.kv.element_size()
+
+
+def export_kv(runner, seq: Sequence) -> KVSnapshot:
+    """Snapshot a running request between steps (kv_handoff.py:34-59)."""
+    if runner.world_size != 1:
+        raise NotImplementedError("KV handoff currently requires tensor_parallel_size=1")
+    if seq.status != SequenceStatus.RUNNING or seq.num_scheduled_tokens:
+        raise ValueError("export requires a running sequence between steps")
+    count = seq.num_cached_tokens
+    if count <= 0 or count != len(seq) - 1:
+        raise ValueError("export requires exactly one pending, uncached token")
+    num_blocks = -(-count // runner.block_size)
+    if len(seq.block_table) < num_blocks:
+        raise ValueError("sequence is missing KV blocks")
+    pool = runner.kv_cache
+    dense = torch.empty((2, pool.shape[1], count, *pool.shape[-2:]), dtype=pool.dtype, device=pool.device)
+    ops.gather_tokens(pool, seq.block_table[:num_blocks], count, dense)
+    payload = dense.cpu()
+    return KVSnapshot(seq.token_ids.copy(), seq.num_prompt_tokens, count, runner.block_size, seq.temperature,
+                      seq.max_tokens, seq.ignore_eos, payload)
+
+
+def verify_imported_kv(runner, seq: Sequence, snapshot: KVSnapshot) -> bool:
+    """Byte-compare the imported blocks with the snapshot, one block at a time (kv_handoff.py:62-77)."""
+    pool = runner.kv_cache
+    for logical, physical in enumerate(seq.block_table):
+        start = logical * runner.block_size
+        end = min(start + runner.block_size, snapshot.num_cached_tokens)
+        if end <= start:
+            break
+        actual = pool[:, :, physical, :end - start].cpu()
+        expected = snapshot.kv[:, :, start:end]
+        if not torch.equal(actual.view(torch.uint8), expected.contiguous().view(torch.uint8)):
+            return False
+    return True
+
+
+def import_kv(runner, block_manager, snapshot: KVSnapshot) -> Sequence:
+    """Allocate fresh blocks and rebuild a decode-ready sequence (kv_handoff.py:80-135).
+
+    Failure after allocation releases the blocks; prefix hashes are published
+    only after the scatter is queued.
+    """
+    if runner.world_size != 1:
+        raise NotImplementedError("KV handoff currently requires tensor_parallel_size=1")
+    pool = runner.kv_cache
+    expected = (2, pool.shape[1], snapshot.num_cached_tokens, *pool.shape[-2:])
+    if (snapshot.block_size != runner.block_size or block_manager.block_size != runner.block_size
+            or tuple(snapshot.kv.shape) != expected or snapshot.kv.dtype != pool.dtype
+            or snapshot.kv.device.type != "cpu"):
+        raise ValueError("snapshot layout, dtype or block size does not match this worker")
+    if (not 0 < snapshot.num_prompt_tokens < len(snapshot.token_ids)
+            or snapshot.num_cached_tokens != len(snapshot.token_ids) - 1
+            or len(snapshot.token_ids) - snapshot.num_prompt_tokens >= snapshot.max_tokens):
+        raise ValueError("snapshot must contain an unfinished completion and one uncached token")
+    seq = Sequence(snapshot.token_ids[:snapshot.num_prompt_tokens],
+                   SamplingParams(temperature=snapshot.temperature, max_tokens=snapshot.max_tokens,
+                                  ignore_eos=snapshot.ignore_eos))
+    for token in snapshot.token_ids[snapshot.num_prompt_tokens:]:
+        seq.append_token(token)
+    block_manager.allocate_for_resume(seq, snapshot.num_cached_tokens)
+    try:
+        payload = snapshot.kv.to(device=pool.device)
+        ops.scatter_tokens(pool, seq.block_table, snapshot.num_cached_tokens, payload.contiguous())
+        # Prefix metadata becomes valid only once the payload's copy is queued.
+        seq.num_cached_tokens = 0
+        seq.num_scheduled_tokens = snapshot.num_cached_tokens
+        block_manager.hash_blocks(seq)
+        seq.num_scheduled_tokens = 0
+        seq.num_cached_tokens = snapshot.num_cached_tokens
+        seq.status = SequenceStatus.RUNNING
+        seq.is_prefill = False
+    except BaseException:
+        block_manager.deallocate(seq)
+        raise
+    return seq

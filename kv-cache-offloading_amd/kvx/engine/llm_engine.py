@@ -11,6 +11,9 @@ tensor-parallel workers is the runner's business and outside this package.
 
 from dataclasses import dataclass, fields
 
+import torch
+
+from kvx.engine import kv_handoff
 from kvx.engine.cpu_prefix_cache import CPUBlockCache
 from kvx.engine.scheduler import Scheduler, validate_scheduling_options
 from kvx.engine.sequence import SamplingParams, Sequence
@@ -71,11 +74,14 @@ class LLMEngine:
         self.tokenizer = tokenizer
         self.scheduler = Scheduler(config)
         self._cpu_prefix_cache: CPUBlockCache | None = None
+        self._detached_requests: dict[int, Sequence] = {}
 
     def exit(self):
         cache = getattr(self, "_cpu_prefix_cache", None)
         if cache is not None:
             cache.close()
+        for seq_id in tuple(self._detached_requests):
+            self.release_detached_request(seq_id)
         call = getattr(self.model_runner, "call", None)
         if call is not None:
             call("exit")
@@ -116,6 +122,47 @@ class LLMEngine:
         if not isinstance(prefix, Sequence):
             prefix = Sequence(prefix)
         return self.scheduler.block_manager.prefetch(prefix, reserve=len(self.scheduler.running))
+
+    # -- KV handoff between engines (llm_engine.py:127-173) -------------------
+
+    def detach_request(self, seq_id: int) -> kv_handoff.KVSnapshot:
+        """Export a running request's KV and take it out of scheduling; its blocks stay owned."""
+        if seq_id in self._detached_requests:
+            raise ValueError(f"request {seq_id} is already detached")
+        seq = next((seq for seq in self.scheduler.running if seq.seq_id == seq_id), None)
+        if seq is None:
+            raise ValueError(f"request {seq_id} is not running at a handoff boundary")
+        snapshot = kv_handoff.export_kv(self.model_runner, seq)
+        self._detached_requests[seq_id] = seq
+        self.scheduler.running.remove(seq)
+        return snapshot
+
+    def release_detached_request(self, seq_id: int):
+        seq = self._detached_requests[seq_id]
+        self.scheduler.block_manager.deallocate(seq)
+        del self._detached_requests[seq_id]
+
+    def reattach_request(self, seq_id: int) -> int:
+        seq = self._detached_requests[seq_id]
+        self.scheduler.running.append(seq)
+        del self._detached_requests[seq_id]
+        return seq.seq_id
+
+    def resume_request(self, snapshot: kv_handoff.KVSnapshot) -> int:
+        """Import a snapshot as a running request; admit it only once its KV is on the device."""
+        manager = self.scheduler.block_manager
+        seq = None
+        try:
+            seq = kv_handoff.import_kv(self.model_runner, manager, snapshot)
+            device = self.model_runner.kv_cache.device
+            if device.type == "cuda":
+                torch.cuda.synchronize(device)
+            self.scheduler.running.append(seq)
+        except Exception:
+            if seq is not None:
+                manager.deallocate(seq)
+            raise
+        return seq.seq_id
 
     def step(self):
         result = self._step(emit_events=False)

@@ -215,3 +215,38 @@ def selftest(device=None) -> dict[str, int]:
     counters = torch.zeros(8, dtype=torch.int64, device=device)
     check(lib().kvx_selftest(counters.data_ptr(), _stream(device)), "selftest")
     return dict(zip(SELFTEST_FIELDS, counters.cpu().tolist()))
+
+
+# ---------------------------------------------------------------------------
+# Token-granular copies (KV handoff)
+
+def _token_copy(gather: bool, pool: torch.Tensor, block_table, num_tokens: int, dense: torch.Tensor, stream=None):
+    if pool.ndim != 6:
+        raise ValueError("pool must be [2, layers, blocks, block_size, heads, head_dim]")
+    expected = (2, pool.shape[1], num_tokens, *pool.shape[-2:])
+    if tuple(dense.shape) != expected or dense.dtype != pool.dtype or not dense.is_contiguous():
+        raise ValueError(f"dense buffer must be a contiguous {pool.dtype} tensor of shape {expected}")
+    if dense.device.type == "cuda":
+        _require_device(pool, dense)
+    elif not dense.is_pinned():
+        raise ValueError("a host buffer must be pinned (device-accessible)")
+    device = _require_device(pool)
+    table = list(block_table)
+    fn = lib().kvx_gather_tokens if gather else lib().kvx_scatter_tokens
+    check(fn(pool.data_ptr(), ctypes.byref(pool_layout(pool)), int32_array(table), len(table),
+             num_tokens * pool.shape[4], dense.data_ptr(), _stream(device, stream)),
+          "gather_tokens" if gather else "scatter_tokens")
+
+
+def gather_tokens(pool: torch.Tensor, block_table, num_tokens: int, out: torch.Tensor, stream=None):
+    """out[:, :, t] = pool[:, :, block_table[t // BS], t % BS] for t < num_tokens.
+
+    `out` is [2, L, num_tokens, H, hd] (kv_handoff.py:46-55's packed payload),
+    on the pool's device or in pinned host memory.
+    """
+    _token_copy(True, pool, block_table, num_tokens, out, stream)
+
+
+def scatter_tokens(pool: torch.Tensor, block_table, num_tokens: int, src: torch.Tensor, stream=None):
+    """pool[:, :, block_table[t // BS], t % BS] = src[:, :, t] for t < num_tokens (kv_handoff.py:112-118)."""
+    _token_copy(False, pool, block_table, num_tokens, src, stream)

@@ -1,0 +1,128 @@
+"""Negative controls for the copy engine's ordering rules.
+
+Each test drops exactly one rule (kvx_cache_set_debug) in a scenario where a
+delay kernel on one copy stream makes the unordered access overtake the other,
+and asserts that the bytes come out wrong. The matching positive tests
+(test_gpu_cache.py, test_gpu_engine.py) pass with every rule in place, so these
+show those tests would catch a missing wait. The reference claims such
+controls (README.md:114-117) but commits none.
+
+The slot-read rule (a save waits for restores still reading its host slot)
+has no control here: with the rule dropped, the HIP runtime still ran the
+save's device-to-host copy after the delayed restore's host-to-device copy of
+the same slot (both small copies were served in order by one DMA queue), so
+the race it guards against could not be provoked on this platform. The rule
+stays in place because that ordering is not guaranteed.
+"""
+
+from collections import deque
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import u8
+from kvx import _lib, ops
+from kvx.engine.block_manager import BlockManager
+from kvx.engine.cpu_prefix_cache import CPUBlockCache
+
+pytestmark = pytest.mark.gpu
+BS = 256
+
+
+def pool_with_bytes(device, blocks):
+    pool = torch.empty((2, 2, blocks, BS, 1, 4), dtype=torch.bfloat16, device=device)
+    raw = torch.arange(pool.numel() * 2, device=device).remainder(251).to(torch.uint8)
+    pool.view(torch.uint8).copy_(raw.view(pool.view(torch.uint8).shape))
+    return pool
+
+
+def publish(manager, block_id, token):
+    tokens = [token] * BS
+    h = manager.compute_hash(tokens)
+    manager.blocks[block_id].update(h, tokens)
+    manager.hash_to_block_id[h] = block_id
+    return h
+
+
+def forget(manager, key):
+    block_id = manager.hash_to_block_id.pop(key)
+    manager.blocks[block_id].hash, manager.blocks[block_id].token_ids = -1, []
+
+
+def cache_for(pool, manager, blocks, **kwargs):
+    size = pool[:, :, 0].numel() * pool.element_size()
+    runner = SimpleNamespace(world_size=1, block_size=BS, kv_cache=pool)
+    return CPUBlockCache(runner, manager, blocks * size, **kwargs)
+
+
+def delay(stream, device):
+    ops.sleep(20_000, stream=stream, device=device)
+
+
+def block(pool, b):
+    torch.cuda.synchronize()
+    return u8(pool[:, :, b])
+
+
+def test_restore_reads_a_poisoned_slot_without_the_save_wait(gpu):
+    pool = pool_with_bytes(gpu, 3)
+    manager = BlockManager(3, BS)
+    key = publish(manager, 0, 1)
+    cache = cache_for(pool, manager, 1, split_streams=True, preallocate=True)
+    cache._slab_memory[0].fill_(0xAB)
+    expected = block(pool, 0)
+    cache._engine.set_debug(_lib.DEBUG_SKIP_SAVE_WAIT)
+    delay(cache._copy_stream, gpu)
+    assert cache.save_block(key)
+    forget(manager, key)
+    manager.free_block_ids = deque([1, 2, 0])  # restore into a block no save is pending on
+    target = cache.restore_block(key)
+    cache.synchronize()
+    assert target == 1
+    assert not np.array_equal(block(pool, target), expected)
+    assert np.all(block(pool, target) == 0xAB)  # it copied the poison
+
+
+def test_compute_overwrites_a_block_before_its_save_without_the_reuse_wait(gpu):
+    pool = pool_with_bytes(gpu, 2)
+    manager = BlockManager(2, BS)
+    key = publish(manager, 1, 1)
+    cache = cache_for(pool, manager, 1)
+    expected = block(pool, 1)
+    cache._engine.set_debug(_lib.DEBUG_SKIP_REUSE_WAIT)
+    delay(cache._copy_stream, gpu)
+    assert cache.save_block(key)
+    forget(manager, key)
+    cache.before_block_reuse(1)  # no longer waits for the save
+    pool.fill_(-7)
+    target = cache.restore_block(key)
+    cache.synchronize()
+    assert not np.array_equal(block(pool, target), expected)
+
+
+def test_restore_overwrites_a_victim_before_its_save_without_the_victim_wait(gpu):
+    pool = pool_with_bytes(gpu, 2)
+    manager = BlockManager(2, BS)
+    victim_key = publish(manager, 0, 3)
+    key = publish(manager, 1, 4)
+    cache = cache_for(pool, manager, 2, automatic=True, split_streams=True)
+    victim_bytes = block(pool, 0)
+    assert cache.save_block(key)
+    cache.synchronize()
+    forget(manager, key)
+    cache._engine.set_debug(_lib.DEBUG_SKIP_VICTIM_WAIT)
+    original = cache._save_to_slot
+
+    def slow_save(block_id, slot):
+        delay(cache._copy_stream, gpu)
+        original(block_id, slot)
+
+    cache._save_to_slot = slow_save
+    entry = cache._entries[key]
+    target = manager.restore_cached_block(key, entry.token_ids,
+                                          lambda b: cache._copy_entry(entry, b, wait=False))
+    assert target == 0 and victim_key in cache
+    cache.synchronize()
+    assert not np.array_equal(u8(cache._entries[victim_key].kv), victim_bytes)
