@@ -51,6 +51,7 @@ def parse_args():
     p.add_argument("--skip-host-link", action="store_true")
     p.add_argument("--skip-cpu-baseline", action="store_true")
     p.add_argument("--skip-store", action="store_true", help="skip the store_kvcache leg")
+    p.add_argument("--skip-hybrid", action="store_true", help="skip the hybrid-admission calibration leg")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample budget")
     p.add_argument("--host-reps", type=int, default=3)
     p.add_argument("--calibrate-copy", action="store_true",
@@ -146,9 +147,51 @@ def store_leg(torch, ops, pool, reps=5):
     row = heads * hd * 2
     per_launch = total * 4 * row + padded * 4  # K and V rows read and written, plus the slot map
     gbs = layers * per_launch / t / 1e9
+    traffic, _ = pmc_traffic("store_kv_vec<")
     return {"tokens": total, "padded_tokens": padded, "layers": layers, "ms_all_layers": round(1000 * t, 4),
             "algorithmic_bytes_per_launch": per_launch, "hbm_gbs": round(gbs, 1),
-            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic}
+
+
+# Recompute cost coefficients the reference's replay harness defaults to
+# (bench/agent_replay.py:283-286); they describe the model, not this path.
+RECOMPUTE_S_PER_TOKEN = 6.87e-6
+RECOMPUTE_S_PER_TOKEN2 = 9.3e-10
+
+
+def hybrid_leg(torch, pool, scale_dtype, prefix_blocks=128):
+    """The hybrid-admission calibration loop (bench/agent_replay.py:387-391) on this path.
+
+    Measures the restore cost per block (H2D DMA plus dequantisation) with
+    CPUBlockCache.measure_restore_s_per_block, sets cache.hybrid from it, and
+    reports the split plan_split picks for a 32,768-token prefix.
+    """
+    from types import SimpleNamespace
+
+    from kvx.engine.block_manager import BlockManager, plan_split
+    from kvx.engine.cpu_prefix_cache import CPUBlockCache
+
+    _, _, nb, bs, _, _ = pool.shape
+    runner = SimpleNamespace(world_size=1, block_size=bs, kv_cache=pool)
+    out = {"prefix_blocks": prefix_blocks, "recompute_s_per_token": RECOMPUTE_S_PER_TOKEN,
+           "recompute_s_per_token2": RECOMPUTE_S_PER_TOKEN2}
+    for name, fp8 in (("fp8", True), ("bf16", False)):
+        cache = CPUBlockCache(runner, BlockManager(nb, bs), 1 << 30, automatic=True, fp8=fp8,
+                              scale_dtype=scale_dtype if fp8 else None)
+        try:
+            restore_s = cache.measure_restore_s_per_block()
+            cache.hybrid = (restore_s, RECOMPUTE_S_PER_TOKEN, RECOMPUTE_S_PER_TOKEN2)
+            split = plan_split(prefix_blocks, bs, *cache.hybrid)
+        finally:
+            cache.close()
+        tokens = split * bs
+        recompute = tokens * RECOMPUTE_S_PER_TOKEN + tokens * tokens * RECOMPUTE_S_PER_TOKEN2
+        out[name] = {"restore_ms_per_block": round(1000 * restore_s, 4),
+                     "restore_gbs": round(cache.block_bytes / restore_s / 1e9, 2),
+                     "recompute_blocks": split, "restored_blocks": prefix_blocks - split,
+                     "admission_ms": round(1000 * max(recompute, (prefix_blocks - split) * restore_s), 3),
+                     "restore_only_ms": round(1000 * prefix_blocks * restore_s, 3)}
+    return out
 
 
 def host_link_leg(torch, pool, layout, sources, dests, reps):
@@ -379,6 +422,9 @@ def main():
         log("host link leg")
         result["host_link"] = host_link_leg(torch, pool, ops.pool_layout(pool, scale_dtype), sources, dests,
                                             args.host_reps)
+    if not args.skip_hybrid:
+        log("hybrid calibration leg")
+        result["hybrid_admission"] = hybrid_leg(torch, pool, scale_dtype)
     if not args.skip_cpu_baseline:
         log("cpu baseline leg")
         result["cpu_baseline"] = cpu_baseline_leg(torch, shape, scale_dtype, args.cpu_seconds)

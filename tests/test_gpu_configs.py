@@ -19,7 +19,7 @@ import torch
 
 from helpers import bf16_bits, u8
 from kvx import ops
-from kvx.engine.block_manager import BlockManager
+from kvx.engine.block_manager import BlockManager, plan_split
 from kvx.engine.cpu_prefix_cache import CPUBlockCache
 from kvx.engine.sequence import SamplingParams, Sequence
 from kvx.workloads import QWEN3_0_6B, QWEN3_8B, block_selection, fill_normal, fill_student_t
@@ -141,6 +141,44 @@ def test_config3_hybrid_admission_restores_only_the_tail(gpu):
     for i in range(13):
         assert torch.equal(pool[:, :, seq.block_table[i]].view(torch.int16), canary), f"head block {i} written"
     for i in range(13, 128):
+        assert same_bytes(pool[:, :, seq.block_table[i]], originals[:, :, i]), f"tail block {i}"
+    manager.deallocate(seq)
+    cache.close()
+
+
+def test_hybrid_split_follows_the_measured_restore_cost(gpu):
+    """The calibration loop of bench/agent_replay.py:387-391: measure, set hybrid, admit."""
+    pool = random_bits_pool(QWEN3_8B.shape, gpu, seed=11)
+    manager = BlockManager(QWEN3_8B.num_blocks, BS)
+    n = 128
+    sources = block_selection(QWEN3_8B.num_blocks, n, seed=12)
+    tokens = [t for i in range(n) for t in [3000 + i] * BS]
+    keys, h = [], -1
+    for i, b in enumerate(sources):
+        h = publish(manager, b, tokens[i * BS:(i + 1) * BS], h)
+        keys.append(h)
+    originals = pool[:, :, sources].clone()
+    block_bytes = pool[:, :, 0].numel() * pool.element_size()
+    cache = CPUBlockCache(runner_for(pool), manager, n * block_bytes, automatic=True, split_streams=True)
+    restore_s = cache.measure_restore_s_per_block()
+    # One BF16 block over a PCIe 5.0 x16 link: about 0.6-0.7 ms.
+    assert 0.3e-3 < restore_s < 3e-3, restore_s
+    cache.hybrid = (restore_s, 6.87e-6, 9.3e-10)  # recompute costs: agent_replay.py:283-286 defaults
+    split = plan_split(n, BS, *cache.hybrid)
+    assert 0 < split < n
+    for key in keys:
+        cache.save_block(key)
+    cache.synchronize()
+    for key in keys:
+        forget(manager, key)
+    seq = Sequence(tokens + [7], SamplingParams(temperature=0, max_tokens=1))
+    manager.allocate(seq, manager.can_allocate(seq))
+    assert seq.restore_span == (split * BS, n * BS)
+    assert cache.stats["restored_blocks"] == n - split
+    seq.num_cached_tokens = split * BS
+    manager.finish_restore_span(seq)
+    cache.synchronize()
+    for i in range(split, n):
         assert same_bytes(pool[:, :, seq.block_table[i]], originals[:, :, i]), f"tail block {i}"
     manager.deallocate(seq)
     cache.close()

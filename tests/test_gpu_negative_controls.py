@@ -85,21 +85,34 @@ def test_restore_reads_a_poisoned_slot_without_the_save_wait(gpu):
     assert np.all(block(pool, target) == 0xAB)  # it copied the poison
 
 
-def test_compute_overwrites_a_block_before_its_save_without_the_reuse_wait(gpu):
+def reuse_race_corrupts(gpu, compute):
+    """One save delayed on the copy stream, then a compute-stream write with the reuse wait dropped."""
     pool = pool_with_bytes(gpu, 2)
     manager = BlockManager(2, BS)
     key = publish(manager, 1, 1)
-    cache = cache_for(pool, manager, 1)
-    expected = block(pool, 1)
-    cache._engine.set_debug(_lib.DEBUG_SKIP_REUSE_WAIT)
-    delay(cache._copy_stream, gpu)
-    assert cache.save_block(key)
-    forget(manager, key)
-    cache.before_block_reuse(1)  # no longer waits for the save
-    pool.fill_(-7)
-    target = cache.restore_block(key)
-    cache.synchronize()
-    assert not np.array_equal(block(pool, target), expected)
+    with torch.cuda.stream(compute):
+        cache = cache_for(pool, manager, 1)
+        expected = block(pool, 1)
+        cache._engine.set_debug(_lib.DEBUG_SKIP_REUSE_WAIT)
+        delay(cache._copy_stream, gpu)
+        assert cache.save_block(key)
+        forget(manager, key)
+        cache.before_block_reuse(1)  # no longer waits for the save
+        pool.fill_(-7)
+        target = cache.restore_block(key)
+        cache.synchronize()
+        corrupted = not np.array_equal(block(pool, target), expected)
+    cache.close()
+    return corrupted
+
+
+def test_compute_overwrites_a_block_before_its_save_without_the_reuse_wait(gpu):
+    # Streams share the process's few hardware queues; a compute stream that
+    # lands on the copy stream's queue runs its write after the delay kernel
+    # in queue order, which hides the race. Four consecutive pool streams
+    # cannot all share the copy stream's queue, so one of them shows it.
+    candidates = [torch.cuda.default_stream(gpu)] + [torch.cuda.Stream(gpu) for _ in range(4)]
+    assert any(reuse_race_corrupts(gpu, s) for s in candidates)
 
 
 def test_restore_overwrites_a_victim_before_its_save_without_the_victim_wait(gpu):
