@@ -52,6 +52,7 @@ def parse_args():
     p.add_argument("--skip-cpu-baseline", action="store_true")
     p.add_argument("--skip-store", action="store_true", help="skip the store_kvcache leg")
     p.add_argument("--skip-hybrid", action="store_true", help="skip the hybrid-admission calibration leg")
+    p.add_argument("--skip-agents", action="store_true", help="skip the agent-pressure leg")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample budget")
     p.add_argument("--host-reps", type=int, default=3)
     p.add_argument("--calibrate-copy", action="store_true",
@@ -194,6 +195,35 @@ def hybrid_leg(torch, pool, scale_dtype, prefix_blocks=128):
     return out
 
 
+def agent_leg(torch, pool, scale_dtype):
+    """Agent pressure through the whole engine: 4 agents x 32,768-token contexts, 12 turns of 2,048 new tokens.
+
+    FP8 saves of evicted blocks into an 8 GiB pinned budget, restores and
+    prefetch restores of each returning agent's prefix, KV written by
+    store_kvcache. Run once with split save/restore streams and once with one
+    copy stream; link GB/s is entry bytes moved over the run's wall time
+    (engine, scheduling and the synthetic model included).
+    """
+    from kvx.engine.llm_engine import LLMEngine
+    from kvx.workloads import SyntheticKVRunner, run_agent_pressure
+
+    out = {"agents": 4, "context_tokens": 32768, "turns": 12, "append_tokens": 2048, "host_budget_bytes": 8 << 30}
+    for name, split in (("split_streams", True), ("one_copy_stream", False)):
+        engine = LLMEngine(SyntheticKVRunner(pool), max_num_batched_tokens=16384, max_num_seqs=4, eos=-1,
+                           kvcache_block_size=pool.shape[3], num_kvcache_blocks=pool.shape[2])
+        engine.create_cpu_prefix_cache(8 << 30, automatic=True, prefetch=True, split_streams=split, fp8=True,
+                                       scale_dtype=scale_dtype)
+        try:
+            r = run_agent_pressure(engine, agents=4, context=32768, turns=12, append=2048, verify=False)
+        finally:
+            engine.exit()
+        out[name] = {"wall_s": round(r.wall_s, 3), "saved_blocks": r.saved_blocks,
+                     "restored_blocks": r.restored_blocks, "prefetched_blocks": r.prefetched_blocks,
+                     "d2h_bytes": r.d2h_bytes, "h2d_bytes": r.h2d_bytes, "link_gbs": round(r.link_gbs, 2)}
+    out["split_speedup"] = round(out["one_copy_stream"]["wall_s"] / out["split_streams"]["wall_s"], 3)
+    return out
+
+
 def host_link_leg(torch, pool, layout, sources, dests, reps):
     """Saves to / restores from pinned host slabs through the copy engine; D2H, H2D, both at once."""
     from kvx import ops
@@ -237,10 +267,10 @@ def host_link_leg(torch, pool, layout, sources, dests, reps):
 
         both_s = timed(both)
 
-        # Ceiling: contiguous pinned hipMemcpyAsync each way, and both at once
-        # on the engine's two streams (the runtime torch loaded), in 16
-        # interleaved pieces per direction (one multi-GB copy per stream does
-        # not always overlap with the other direction).
+        # Ceiling: pinned hipMemcpyAsync each way, and both at once on the
+        # engine's two streams (the runtime torch loaded), interleaved in pieces
+        # (one multi-GB copy per stream does not always overlap with the other
+        # direction); the best of several piece sizes is the ceiling.
         hip = ctypes.CDLL("libamdhip64.so.7")
         hip.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
                                        ctypes.c_void_p]
@@ -249,27 +279,26 @@ def host_link_leg(torch, pool, layout, sources, dests, reps):
         host_a, host_b = slab.data_ptr(), slab.data_ptr() + n * stride
         s1, s2 = engine.save_stream.cuda_stream, engine.restore_stream.cuda_stream
 
-        piece = -(-link_bytes // 16)
-
-        def pieces():
+        def pieces(piece):
             return [(off, min(piece, link_bytes - off)) for off in range(0, link_bytes, piece)]
 
-        def d2h():
-            for off, size in pieces():
+        def d2h(piece):
+            for off, size in pieces(piece):
                 assert hip.hipMemcpyAsync(host_a + off, flat_dev.data_ptr() + off, size, 2, s1) == 0
 
-        def h2d():
-            for off, size in pieces():
+        def h2d(piece):
+            for off, size in pieces(piece):
                 assert hip.hipMemcpyAsync(flat_dev2.data_ptr() + off, host_b + off, size, 1, s2) == 0
 
-        def both_ways():
-            for (off, size) in pieces():
+        def both_ways(piece):
+            for (off, size) in pieces(piece):
                 assert hip.hipMemcpyAsync(host_a + off, flat_dev.data_ptr() + off, size, 2, s1) == 0
                 assert hip.hipMemcpyAsync(flat_dev2.data_ptr() + off, host_b + off, size, 1, s2) == 0
 
-        ceil_d2h = timed(d2h)
-        ceil_h2d = timed(h2d)
-        ceil_both = timed(both_ways)
+        piece_sizes = (8 << 20, 16 << 20, 32 << 20, 64 << 20, -(-link_bytes // 16))
+        ceil_d2h = min(timed(lambda: d2h(p)) for p in piece_sizes)
+        ceil_h2d = min(timed(lambda: h2d(p)) for p in piece_sizes)
+        ceil_both = min(timed(lambda: both_ways(p)) for p in piece_sizes)
         gbs = lambda nbytes, s: nbytes / s / 1e9  # noqa: E731
         overlap = (save_s + restore_s - both_s) / min(save_s, restore_s)
         duplex = gbs(2 * link_bytes, both_s)
@@ -425,6 +454,9 @@ def main():
     if not args.skip_hybrid:
         log("hybrid calibration leg")
         result["hybrid_admission"] = hybrid_leg(torch, pool, scale_dtype)
+    if not args.skip_agents:
+        log("agent pressure leg")
+        result["agent_pressure"] = agent_leg(torch, pool, scale_dtype)
     if not args.skip_cpu_baseline:
         log("cpu baseline leg")
         result["cpu_baseline"] = cpu_baseline_leg(torch, shape, scale_dtype, args.cpu_seconds)

@@ -260,7 +260,9 @@ struct kvx_cache {
   // slots. Runs of consecutive slots in one slab are merged, then cut into
   // pieces of at most kDmaPiece bytes: two multi-gigabyte copies queued at the
   // same moment on the save and restore streams were measured to serialize
-  // (57 GB/s in total), while the same bytes in pieces ran full duplex (97 GB/s).
+  // (57 GB/s in total), while the same bytes in pieces ran full duplex
+  // (~95 GB/s over PCIe 5.0 for 32-128 MiB pieces; 8 MiB pieces lose 3-4%,
+  // and 16 MiB was best on one host but 1% behind on another).
   static constexpr size_t kDmaPiece = 64u << 20;
   int dma(bool to_host, uint8_t* staging, const int32_t* slots, int32_t count, hipStream_t s) {
     int32_t i = 0;

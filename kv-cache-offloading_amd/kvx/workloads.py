@@ -94,20 +94,29 @@ def block_selection(num_blocks: int, count: int, seed: int, exclude=()) -> list[
 # ---------------------------------------------------------------------------
 # Model-free engine runs
 
-def synthetic_kv(tokens: torch.Tensor, positions: torch.Tensor, layer: int, kv: int, heads: int, head_dim: int,
+def synthetic_kv(tokens: torch.Tensor, positions: torch.Tensor, layers: int, heads: int, head_dim: int,
                  dtype=torch.bfloat16) -> torch.Tensor:
-    """Deterministic K (kv=0) or V (kv=1) rows [n, heads, head_dim] for tokens at positions.
+    """Deterministic K and V rows [2, layers, n, heads, head_dim] for tokens at positions.
 
     A stand-in for a model's projections: any block's expected contents can be
-    recomputed from its tokens and positions alone.
+    recomputed from its tokens and positions alone. All layers come from one
+    broadcast expression per K/V half, so a run costs a few launches per step.
     """
+    dev = tokens.device
     t = tokens.to(torch.float32)[:, None, None]
     p = positions.to(torch.float32)[:, None, None]
-    h = torch.arange(heads, device=tokens.device, dtype=torch.float32)[None, :, None]
-    d = torch.arange(head_dim, device=tokens.device, dtype=torch.float32)[None, None, :]
-    phase = 0.37 * t + 0.0113 * p + 0.71 * h + 0.173 * d + 1.31 * layer + 2.9 * kv
-    amp = 1.0 + 4.0 * (((d.to(torch.int64) * 7 + h.to(torch.int64) * 3 + layer) % 29) == 0)  # outlier channels
-    return (torch.sin(phase) * amp).to(dtype)
+    h = torch.arange(heads, device=dev, dtype=torch.float32)[None, :, None]
+    d = torch.arange(head_dim, device=dev, dtype=torch.float32)[None, None, :]
+    base = 0.37 * t + 0.0113 * p + 0.71 * h + 0.173 * d  # [n, heads, head_dim]
+    layer = torch.arange(layers, device=dev)
+    # Outlier channels: amplitude 5 where (7d + 3h + layer) % 29 == 0.
+    hit = (d.to(torch.int64) * 7 + h.to(torch.int64) * 3 + layer[:, None, None, None]) % 29 == 0
+    amp = 1.0 + 4.0 * hit.to(torch.float32)  # [layers, 1, heads, head_dim]
+    out = torch.empty((2, layers, tokens.numel(), heads, head_dim), dtype=dtype, device=dev)
+    for kv in range(2):
+        offset = (1.31 * layer.to(torch.float64) + 2.9 * kv).to(torch.float32)[:, None, None, None]
+        out[kv] = (torch.sin(base[None] + offset) * amp).to(dtype)
+    return out
 
 
 class SyntheticKVRunner:
@@ -151,11 +160,9 @@ class SyntheticKVRunner:
             t = torch.tensor(toks, device=dev)
             p = torch.tensor(pos, device=dev)
             mapping = torch.tensor(slots, dtype=torch.int32, device=dev)
-            heads, hd = pool.shape[4], pool.shape[5]
+            kv = synthetic_kv(t, p, pool.shape[1], pool.shape[4], pool.shape[5], pool.dtype)
             for layer in range(pool.shape[1]):
-                k = synthetic_kv(t, p, layer, 0, heads, hd, pool.dtype)
-                v = synthetic_kv(t, p, layer, 1, heads, hd, pool.dtype)
-                ops.store_kvcache(k, v, pool[0, layer], pool[1, layer], mapping)
+                ops.store_kvcache(kv[0, layer], kv[1, layer], pool[0, layer], pool[1, layer], mapping)
             self.tokens_written += len(slots)
         return [self.next_token] * len(seqs)
 
@@ -165,9 +172,7 @@ def expected_block(pool: torch.Tensor, token_ids, start_position: int) -> torch.
     dev = pool.device
     t = torch.tensor(list(token_ids), device=dev)
     p = torch.arange(start_position, start_position + len(token_ids), device=dev)
-    heads, hd = pool.shape[4], pool.shape[5]
-    return torch.stack([torch.stack([synthetic_kv(t, p, layer, kv, heads, hd, pool.dtype)
-                                     for layer in range(pool.shape[1])]) for kv in range(2)])
+    return synthetic_kv(t, p, pool.shape[1], pool.shape[4], pool.shape[5], pool.dtype)
 
 
 @dataclass

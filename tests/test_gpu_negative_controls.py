@@ -1,10 +1,10 @@
 """Negative controls for the copy engine's ordering rules.
 
 Each test drops exactly one rule (kvx_cache_set_debug) in a scenario where a
-delay kernel on one copy stream makes the unordered access overtake the other,
-and asserts that the bytes come out wrong. The matching positive tests
-(test_gpu_cache.py, test_gpu_engine.py) pass with every rule in place, so these
-show those tests would catch a missing wait. The reference claims such
+delay kernel on one copy stream lets the unordered access overtake the other,
+and asserts that the bytes come out wrong in at least one of a few attempts.
+The matching positive tests (test_gpu_cache.py, test_gpu_engine.py) pass with
+every rule in place, so these show those tests would catch a missing wait. The reference claims such
 controls (README.md:114-117) but commits none.
 
 The slot-read rule (a save waits for restores still reading its host slot)
@@ -66,7 +66,20 @@ def block(pool, b):
     return u8(pool[:, :, b])
 
 
-def test_restore_reads_a_poisoned_slot_without_the_save_wait(gpu):
+# The HIP runtime maps every stream onto one of the process's few hardware
+# queues, and a delay kernel holds up everything queued behind it on its
+# queue. When the two streams of a scenario share a queue, the unordered
+# access runs in queue order and the race stays hidden. Each scenario
+# therefore runs on fresh caches, whose streams come from the next torch pool
+# slots, until one attempt shows the race; the control requires that one does.
+ATTEMPTS = 6
+
+
+def shows_race(scenario, *args):
+    return any(scenario(*args) for _ in range(ATTEMPTS))
+
+
+def restore_without_save_wait(gpu):
     pool = pool_with_bytes(gpu, 3)
     manager = BlockManager(3, BS)
     key = publish(manager, 0, 1)
@@ -81,11 +94,19 @@ def test_restore_reads_a_poisoned_slot_without_the_save_wait(gpu):
     target = cache.restore_block(key)
     cache.synchronize()
     assert target == 1
-    assert not np.array_equal(block(pool, target), expected)
-    assert np.all(block(pool, target) == 0xAB)  # it copied the poison
+    got = block(pool, target)
+    cache.close()
+    if np.array_equal(got, expected):
+        return False
+    assert np.all(got == 0xAB)  # it copied the poison
+    return True
 
 
-def reuse_race_corrupts(gpu, compute):
+def test_restore_reads_a_poisoned_slot_without_the_save_wait(gpu):
+    assert shows_race(restore_without_save_wait, gpu)
+
+
+def reuse_without_reuse_wait(gpu, compute):
     """One save delayed on the copy stream, then a compute-stream write with the reuse wait dropped."""
     pool = pool_with_bytes(gpu, 2)
     manager = BlockManager(2, BS)
@@ -107,15 +128,12 @@ def reuse_race_corrupts(gpu, compute):
 
 
 def test_compute_overwrites_a_block_before_its_save_without_the_reuse_wait(gpu):
-    # Streams share the process's few hardware queues; a compute stream that
-    # lands on the copy stream's queue runs its write after the delay kernel
-    # in queue order, which hides the race. Four consecutive pool streams
-    # cannot all share the copy stream's queue, so one of them shows it.
-    candidates = [torch.cuda.default_stream(gpu)] + [torch.cuda.Stream(gpu) for _ in range(4)]
-    assert any(reuse_race_corrupts(gpu, s) for s in candidates)
+    # The compute stream matters here too: torch's default stream first, then pool streams.
+    candidates = [torch.cuda.default_stream(gpu)] + [torch.cuda.Stream(gpu) for _ in range(ATTEMPTS - 1)]
+    assert any(reuse_without_reuse_wait(gpu, s) for s in candidates)
 
 
-def test_restore_overwrites_a_victim_before_its_save_without_the_victim_wait(gpu):
+def restore_without_victim_wait(gpu):
     pool = pool_with_bytes(gpu, 2)
     manager = BlockManager(2, BS)
     victim_key = publish(manager, 0, 3)
@@ -138,4 +156,10 @@ def test_restore_overwrites_a_victim_before_its_save_without_the_victim_wait(gpu
                                           lambda b: cache._copy_entry(entry, b, wait=False))
     assert target == 0 and victim_key in cache
     cache.synchronize()
-    assert not np.array_equal(u8(cache._entries[victim_key].kv), victim_bytes)
+    corrupted = not np.array_equal(u8(cache._entries[victim_key].kv), victim_bytes)
+    cache.close()
+    return corrupted
+
+
+def test_restore_overwrites_a_victim_before_its_save_without_the_victim_wait(gpu):
+    assert shows_race(restore_without_victim_wait, gpu)
