@@ -151,6 +151,44 @@ def test_fp8_block_save_and_restore_match_the_oracle(gpu, geometry, scale_dtype)
     assert torch.equal(pool[:, :, untouched], canary[:, :, untouched])
 
 
+def ulp_distance(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """|a - b| in units in the last place, for finite non-negative floats of one dtype (ordered as integers)."""
+    itype = torch.int32 if a.dtype == torch.float32 else torch.int16
+    return (a.view(itype).to(torch.int64) - b.view(itype).to(torch.int64)).abs()
+
+
+@pytest.mark.parametrize("scale_dtype", [torch.float32, torch.bfloat16])
+def test_fp8_kernels_match_the_reference_torch_chain_on_the_gpu(gpu, scale_dtype):
+    """Same seeded blocks through kvx and through the reference's own torch ops (cpu_prefix_cache.py:20-28)
+    on this GPU: scales within 1 ulp, payload bit-exact given identical scales, restore bit-exact."""
+    from oracle import torch_path
+
+    pool = make_pool(gpu, layers=36, blocks=4)  # Qwen3-8B block shape, Student-t values
+    g = torch.Generator(device=gpu).manual_seed(9)
+    bits = torch.randint(-32768, 32768, pool[:, :, 3].shape, generator=g, device=gpu, dtype=torch.int32)
+    bits = torch.where((bits & 0x7F80) == 0x7F80, bits & ~0x4000, bits)  # finite bf16 bit patterns only
+    pool[:, :, 3] = bits.to(torch.int16).view(torch.bfloat16)
+    for b in range(4):
+        source = pool[:, :, b]
+        ours_p = torch.empty(source.shape, dtype=torch.float8_e4m3fn, device=gpu)
+        ours_s = torch.empty((*source.shape[:-1], 1), dtype=scale_dtype, device=gpu)
+        ops.fp8_quantize(source, ours_p, ours_s)
+        ref_p, ref_s = torch.empty_like(ours_p), torch.empty_like(ours_s)
+        torch_path.fp8_quantize(source, ref_p, ref_s)
+        assert int(ulp_distance(ours_s, ref_s).max()) <= 1, f"block {b}: scales more than 1 ulp apart"
+        same = (ours_s == ref_s).squeeze(-1)
+        assert torch.equal(ours_p.view(torch.uint8)[same], ref_p.view(torch.uint8)[same]), f"block {b}"
+        # Where a scale differs, the reference's payload formula with our scale gives our codes.
+        if not bool(same.all()):
+            redo = torch.empty_like(ref_p)
+            redo.copy_((source.float() / ours_s.float()).clamp_(-448.0, 448.0))
+            assert torch.equal(ours_p.view(torch.uint8), redo.view(torch.uint8)), f"block {b}"
+        ours_t, ref_t = torch.empty_like(source), torch.empty_like(source)
+        ops.fp8_dequantize(ours_p, ours_s, ours_t)
+        torch_path.fp8_dequantize(ours_p, ours_s, ref_t)
+        assert torch.equal(ours_t.view(torch.int16), ref_t.view(torch.int16)), f"block {b} restore"
+
+
 def byte_pattern_pool(device, shape=(2, 3, 9, 256, 2, 64)):
     """Pool bytes i % 256: every bf16 bit pattern class, NaNs included (test_cpu_prefix_cache.py:15-18)."""
     pool = torch.empty(shape, dtype=torch.bfloat16, device=device)
