@@ -53,6 +53,8 @@ def parse_args():
     p.add_argument("--skip-store", action="store_true", help="skip the store_kvcache leg")
     p.add_argument("--skip-hybrid", action="store_true", help="skip the hybrid-admission calibration leg")
     p.add_argument("--skip-agents", action="store_true", help="skip the agent-pressure leg")
+    p.add_argument("--skip-configs", action="store_true",
+                   help="skip the Qwen3-0.6B FP8 and Qwen3-8B BF16 legs")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample budget")
     p.add_argument("--host-reps", type=int, default=3)
     p.add_argument("--calibrate-copy", action="store_true",
@@ -224,13 +226,81 @@ def agent_leg(torch, pool, scale_dtype):
     return out
 
 
-def host_link_leg(torch, pool, layout, sources, dests, reps):
+def timed_pair(torch, first, second, reps=10):
+    """Median event times (s) of two launches queued back to back on the current stream."""
+    stream = torch.cuda.current_stream()
+    first(), second()
+    t1, t2 = [], []
+    for _ in range(reps):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        ev[0].record(stream)
+        first()
+        ev[1].record(stream)
+        second()
+        ev[2].record(stream)
+        ev[2].synchronize()
+        t1.append(ev[0].elapsed_time(ev[1]) / 1000)
+        t2.append(ev[1].elapsed_time(ev[2]) / 1000)
+    return sorted(t1)[reps // 2], sorted(t2)[reps // 2]
+
+
+def bf16_leg(torch, ops, pool, reps):
+    """BF16 storage mode on the Qwen3-8B pool: byte gather of 200 seeded blocks into entries and scatter into a
+    seeded permutation of the pool (HBM-resident), then 128 + 128 blocks over the host link."""
+    from kvx.workloads import block_selection
+
+    nb = pool.shape[2]
+    sources = block_selection(nb, 200, seed=3)
+    dests = block_selection(nb, 200, seed=4)
+    layout = ops.pool_layout(pool)
+    logical, _, stride = ops.entry_layout(layout, ops.FORMAT_RAW)
+    staging = torch.empty(len(sources) * stride, dtype=torch.uint8, device=pool.device)
+    entries = [staging.data_ptr() + i * stride for i in range(len(sources))]
+    gather_s, scatter_s = timed_pair(torch, lambda: ops.save_blocks(pool, sources, entries, ops.FORMAT_RAW),
+                                     lambda: ops.restore_blocks(pool, dests, entries, ops.FORMAT_RAW))
+    del staging
+    moved = len(sources) * 2 * BF16_BLOCK_BYTES  # read + written per launch
+    order = block_selection(nb, 256, seed=1)
+    link = host_link_leg(torch, pool, layout, order[:128], order[128:], reps, fmt=ops.FORMAT_RAW, ceilings=False)
+    return {"blocks": len(sources), "algorithmic_bytes_per_launch": moved,
+            "gather": {"ms": round(1000 * gather_s, 4), "hbm_gbs": round(moved / gather_s / 1e9, 1),
+                       "frac": round(moved / gather_s / 1e9 / HBM_PEAK_GBS, 4)},
+            "scatter": {"ms": round(1000 * scatter_s, 4), "hbm_gbs": round(moved / scatter_s / 1e9, 1),
+                        "frac": round(moved / scatter_s / 1e9 / HBM_PEAK_GBS, 4)},
+            "host_link_128_blocks": link}
+
+
+def qwen3_0_6b_leg(torch, ops, scale_dtype):
+    """FP8 save of 16 seeded Qwen3-0.6B blocks and restore into 16 other seeded blocks, HBM-resident."""
+    from kvx.workloads import QWEN3_0_6B, block_selection, fill_normal
+
+    pool = torch.empty(QWEN3_0_6B.shape, dtype=torch.bfloat16, device="cuda")
+    fill_normal(pool, seed=0)
+    order = block_selection(QWEN3_0_6B.num_blocks, 32, seed=1)
+    sources, dests = order[:16], order[16:]
+    layout = ops.pool_layout(pool, scale_dtype)
+    logical, _, stride = ops.entry_layout(layout, ops.FORMAT_FP8)
+    staging = torch.empty(16 * stride, dtype=torch.uint8, device=pool.device)
+    entries = [staging.data_ptr() + i * stride for i in range(16)]
+    save_s, restore_s = timed_pair(
+        torch, lambda: ops.save_blocks(pool, sources, entries, ops.FORMAT_FP8, scale_dtype),
+        lambda: ops.restore_blocks(pool, dests, entries, ops.FORMAT_FP8, scale_dtype), reps=20)
+    block = pool[:, :, 0].numel() * 2
+    moved = 16 * (block + logical)
+    del staging, pool
+    return {"pool": list(QWEN3_0_6B.shape), "blocks": 16, "algorithmic_bytes_per_launch": moved,
+            "logical_kv_gbs": round(2 * 16 * block / (save_s + restore_s) / 1e9, 1),
+            "save": {"ms": round(1000 * save_s, 4), "hbm_gbs": round(moved / save_s / 1e9, 1)},
+            "restore": {"ms": round(1000 * restore_s, 4), "hbm_gbs": round(moved / restore_s / 1e9, 1)}}
+
+
+def host_link_leg(torch, pool, layout, sources, dests, reps, fmt=None, ceilings=True):
     """Saves to / restores from pinned host slabs through the copy engine; D2H, H2D, both at once."""
     from kvx import ops
     from kvx.engine.cpu_prefix_cache import _CopyEngine
 
     n = len(sources)
-    engine = _CopyEngine(pool, layout, ops.FORMAT_FP8, split=True)
+    engine = _CopyEngine(pool, layout, ops.FORMAT_FP8 if fmt is None else fmt, split=True)
     try:
         stride = engine.entry_stride
         link_bytes = n * engine.logical_bytes
@@ -267,56 +337,63 @@ def host_link_leg(torch, pool, layout, sources, dests, reps):
 
         both_s = timed(both)
 
-        # Ceiling: pinned hipMemcpyAsync each way, and both at once on the
-        # engine's two streams (the runtime torch loaded), interleaved in pieces
-        # (one multi-GB copy per stream does not always overlap with the other
-        # direction); the best of several piece sizes is the ceiling.
-        hip = ctypes.CDLL("libamdhip64.so.7")
-        hip.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
-                                       ctypes.c_void_p]
-        flat_dev = torch.empty(link_bytes, dtype=torch.uint8, device=pool.device)
-        flat_dev2 = torch.empty_like(flat_dev)
-        host_a, host_b = slab.data_ptr(), slab.data_ptr() + n * stride
-        s1, s2 = engine.save_stream.cuda_stream, engine.restore_stream.cuda_stream
+        ceil_d2h = ceil_h2d = ceil_both = None
+        if ceilings:
+            # Ceiling: pinned hipMemcpyAsync each way, and both at once on the
+            # engine's two streams (the runtime torch loaded), interleaved in pieces
+            # (one multi-GB copy per stream does not always overlap with the other
+            # direction); the best of several piece sizes is the ceiling.
+            hip = ctypes.CDLL("libamdhip64.so.7")
+            hip.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
+                                           ctypes.c_void_p]
+            flat_dev = torch.empty(link_bytes, dtype=torch.uint8, device=pool.device)
+            flat_dev2 = torch.empty_like(flat_dev)
+            host_a, host_b = slab.data_ptr(), slab.data_ptr() + n * stride
+            s1, s2 = engine.save_stream.cuda_stream, engine.restore_stream.cuda_stream
 
-        def pieces(piece):
-            return [(off, min(piece, link_bytes - off)) for off in range(0, link_bytes, piece)]
+            def pieces(piece):
+                return [(off, min(piece, link_bytes - off)) for off in range(0, link_bytes, piece)]
 
-        def d2h(piece):
-            for off, size in pieces(piece):
-                assert hip.hipMemcpyAsync(host_a + off, flat_dev.data_ptr() + off, size, 2, s1) == 0
+            def d2h(piece):
+                for off, size in pieces(piece):
+                    assert hip.hipMemcpyAsync(host_a + off, flat_dev.data_ptr() + off, size, 2, s1) == 0
 
-        def h2d(piece):
-            for off, size in pieces(piece):
-                assert hip.hipMemcpyAsync(flat_dev2.data_ptr() + off, host_b + off, size, 1, s2) == 0
+            def h2d(piece):
+                for off, size in pieces(piece):
+                    assert hip.hipMemcpyAsync(flat_dev2.data_ptr() + off, host_b + off, size, 1, s2) == 0
 
-        def both_ways(piece):
-            for (off, size) in pieces(piece):
-                assert hip.hipMemcpyAsync(host_a + off, flat_dev.data_ptr() + off, size, 2, s1) == 0
-                assert hip.hipMemcpyAsync(flat_dev2.data_ptr() + off, host_b + off, size, 1, s2) == 0
+            def both_ways(piece):
+                for (off, size) in pieces(piece):
+                    assert hip.hipMemcpyAsync(host_a + off, flat_dev.data_ptr() + off, size, 2, s1) == 0
+                    assert hip.hipMemcpyAsync(flat_dev2.data_ptr() + off, host_b + off, size, 1, s2) == 0
 
-        piece_sizes = (8 << 20, 16 << 20, 32 << 20, 64 << 20, -(-link_bytes // 16))
-        ceil_d2h = min(timed(lambda: d2h(p)) for p in piece_sizes)
-        ceil_h2d = min(timed(lambda: h2d(p)) for p in piece_sizes)
-        ceil_both = min(timed(lambda: both_ways(p)) for p in piece_sizes)
+            piece_sizes = (8 << 20, 16 << 20, 32 << 20, 64 << 20, -(-link_bytes // 16))
+            ceil_d2h = min(timed(lambda: d2h(p)) for p in piece_sizes)
+            ceil_h2d = min(timed(lambda: h2d(p)) for p in piece_sizes)
+            ceil_both = min(timed(lambda: both_ways(p)) for p in piece_sizes)
         gbs = lambda nbytes, s: nbytes / s / 1e9  # noqa: E731
         overlap = (save_s + restore_s - both_s) / min(save_s, restore_s)
         duplex = gbs(2 * link_bytes, both_s)
-        return {
+        out = {
             "bytes_per_direction": link_bytes,
             "save_d2h_gbs": round(gbs(link_bytes, save_s), 2),
             "restore_h2d_gbs": round(gbs(link_bytes, restore_s), 2),
             "duplex_gbs": round(duplex, 2),
             "overlap_fraction": round(overlap, 3),
-            "ceiling_memcpy_d2h_gbs": round(gbs(link_bytes, ceil_d2h), 2),
-            "ceiling_memcpy_h2d_gbs": round(gbs(link_bytes, ceil_h2d), 2),
-            "ceiling_memcpy_duplex_gbs": round(gbs(2 * link_bytes, ceil_both), 2),
             "peak_per_direction_gbs": PCIE_PEAK_GBS,
             "frac_duplex_of_spec": round(duplex / (2 * PCIE_PEAK_GBS), 3),
-            "frac_duplex_of_measured_ceiling": round(duplex / gbs(2 * link_bytes, ceil_both), 3),
             "pin_seconds": round(pin_s, 2),
             "logical_kv_gbs": round(2 * n * BF16_BLOCK_BYTES / both_s / 1e9, 2),
+            "streams_concurrent": engine.streams_concurrent,
         }
+        if ceilings:
+            out.update({
+                "ceiling_memcpy_d2h_gbs": round(gbs(link_bytes, ceil_d2h), 2),
+                "ceiling_memcpy_h2d_gbs": round(gbs(link_bytes, ceil_h2d), 2),
+                "ceiling_memcpy_duplex_gbs": round(gbs(2 * link_bytes, ceil_both), 2),
+                "frac_duplex_of_measured_ceiling": round(duplex / gbs(2 * link_bytes, ceil_both), 3),
+            })
+        return out
     finally:
         engine.close()
 
@@ -343,7 +420,21 @@ def cpu_baseline_leg(torch, shape, scale_dtype, seconds):
         elapsed = time.perf_counter() - t0
         if elapsed >= seconds:
             break
+    # The 16-block Qwen3-0.6B round trip (its CPU-runnable configuration), for comparison with the GPU leg.
+    small = (2, 28, 32, 256, 8, 128)
+    small_pool = torch.randn(small, generator=g).to(torch.bfloat16)
+    small_block = (2, 28, 256, 8, 128)
+    small_payload = torch.empty(small_block, dtype=torch.float8_e4m3fn)
+    small_scale = torch.empty((*small_block[:-1], 1), dtype=scale_dtype)
+    t1 = time.perf_counter()
+    for b in range(16):
+        torch_path.save_block(small_pool, b, small_payload, small_scale)
+        torch_path.restore_block(small_pool, 16 + b, small_payload, small_scale)
+    small_s = time.perf_counter() - t1
+    small_bytes = 2 * 16 * small_pool[:, :, 0].numel() * 2
     return {
+        "qwen3_0_6b_16_blocks": {"seconds": round(small_s, 3),
+                                 "logical_kv_gbs": round(small_bytes / small_s / 1e9, 3)},
         "value": round(moved * BF16_BLOCK_BYTES / elapsed / 1e9, 3),
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
@@ -451,6 +542,11 @@ def main():
         log("host link leg")
         result["host_link"] = host_link_leg(torch, pool, ops.pool_layout(pool, scale_dtype), sources, dests,
                                             args.host_reps)
+    if not args.skip_configs:
+        log("bf16 leg")
+        result["bf16_qwen3_8b"] = bf16_leg(torch, ops, pool, args.host_reps)
+        log("qwen3-0.6b leg")
+        result["fp8_qwen3_0_6b"] = qwen3_0_6b_leg(torch, ops, scale_dtype)
     if not args.skip_hybrid:
         log("hybrid calibration leg")
         result["hybrid_admission"] = hybrid_leg(torch, pool, scale_dtype)

@@ -52,20 +52,69 @@ class CPUCacheFullError(MemoryError):
     """The configured payload budget cannot admit another block."""
 
 
+# Copy streams must run side by side with each other and with the compute
+# stream. The HIP runtime maps every stream of a process onto one of a few
+# hardware queues (four by default), and two streams on one queue execute in
+# queue order: with such a pair, saves and restores of 2.5 GB each ran one
+# after the other (55 GB/s in total instead of 94 GB/s full duplex on MI355X),
+# and torch's pool handed out such pairs for every other cache (queues are
+# assigned round-robin at a stream's first use, so every fourth pool stream
+# shares the default stream's). A candidate stream is therefore accepted only
+# after a bounded delay kernel on it overlaps one on each stream already chosen.
+_PROBE_US = 200
+_STREAM_CANDIDATES = 8
+
+
+def _run_side_by_side(a: torch.cuda.Stream, b: torch.cuda.Stream, device: torch.device) -> bool:
+    # A stream's first launch also creates its queue (milliseconds): warm both first.
+    for stream in (a, b):
+        ops.sleep(1, stream=stream, device=device)
+        stream.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    start.record(a)
+    b.wait_event(start)
+    ends = []
+    for stream in (a, b):
+        ops.sleep(_PROBE_US, stream=stream, device=device)
+        end = torch.cuda.Event(enable_timing=True)
+        end.record(stream)
+        ends.append(end)
+    for end in ends:
+        end.synchronize()
+    return max(start.elapsed_time(end) for end in ends) < 1.5 * _PROBE_US / 1000
+
+
+def _copy_streams(device: torch.device, count: int) -> tuple[list[torch.cuda.Stream], bool]:
+    """`count` pool streams that run concurrently with the current stream and each other, if found."""
+    chosen = [torch.cuda.current_stream(device)]
+    concurrent = True
+    for _ in range(count):
+        for _ in range(_STREAM_CANDIDATES):
+            candidate = torch.cuda.Stream(device)
+            ok = all(_run_side_by_side(other, candidate, device) for other in chosen)
+            if ok:
+                break
+        concurrent = concurrent and ok
+        chosen.append(candidate)  # the last candidate still works, only serialised
+    return chosen[1:], concurrent
+
+
 class _CopyEngine:
     """Owner of one kvx_cache handle (events, slab/staging registry).
 
     The engine queues work on two torch streams it borrows, at default
     priority like the reference's (cpu_prefix_cache.py:110-113); torch keeps
     them alive, so torch work queued on them (events, host-allocator
-    bookkeeping) never outlives its stream.
+    bookkeeping) never outlives its stream. The streams are chosen to run
+    concurrently with the caller's stream and each other (_copy_streams).
     """
 
     def __init__(self, pool: torch.Tensor, layout, fmt: int, split: bool):
         self.layout, self.fmt = layout, fmt
         self.logical_bytes, self.scale_offset, self.entry_stride = ops.entry_layout(layout, fmt)
-        self.save_stream = torch.cuda.Stream(pool.device)
-        self.restore_stream = torch.cuda.Stream(pool.device) if split else self.save_stream
+        streams, self.streams_concurrent = _copy_streams(pool.device, 2 if split else 1)
+        self.save_stream = streams[0]
+        self.restore_stream = streams[-1]
         handle = ctypes.c_void_p()
         check(lib().kvx_cache_create(pool.data_ptr(), ctypes.byref(layout), fmt, self.save_stream.cuda_stream,
                                      self.restore_stream.cuda_stream, pool.device.index, ctypes.byref(handle)),
@@ -316,9 +365,11 @@ class CPUBlockCache:
         """Time this cache's restore path (H2D DMA plus FP8 dequantisation) on scratch buffers.
 
         Restores `repeats` zero entries into a one-block scratch pool through a
-        scratch copy engine of the same format, twice (the first pass warms up
-        clocks), and returns seconds per block of the second pass
-        (cpu_prefix_cache.py:245-268).
+        scratch copy engine of the same format: one warm-up pass (kernels and
+        clocks, as cpu_prefix_cache.py:245-268), then three timed passes whose
+        median is returned in seconds per block. One timed pass lasts only a
+        few milliseconds, and single passes measured on MI355X hosts
+        occasionally took 2-8x as long as their neighbours.
         """
         self._require_open()
         device = self._cache.device
@@ -332,14 +383,16 @@ class CPUBlockCache:
             engine.set_staging(staging, staging, 1)
             stream = engine.restore_stream
             compute = torch.cuda.current_stream(device)
-            for _ in range(2):
+            passes = []
+            for _ in range(4):
                 start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 start.record(stream)
                 for i in range(repeats):
                     engine.restore([i], [0], False, compute.cuda_stream)
                 end.record(stream)
                 end.synchronize()
-            return start.elapsed_time(end) / 1000 / repeats
+                passes.append(start.elapsed_time(end) / 1000 / repeats)
+            return sorted(passes[1:])[1]
         finally:
             engine.close()
 

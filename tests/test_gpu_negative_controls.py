@@ -4,15 +4,8 @@ Each test drops exactly one rule (kvx_cache_set_debug) in a scenario where a
 delay kernel on one copy stream lets the unordered access overtake the other,
 and asserts that the bytes come out wrong in at least one of a few attempts.
 The matching positive tests (test_gpu_cache.py, test_gpu_engine.py) pass with
-every rule in place, so these show those tests would catch a missing wait. The reference claims such
-controls (README.md:114-117) but commits none.
-
-The slot-read rule (a save waits for restores still reading its host slot)
-has no control here: with the rule dropped, the HIP runtime still ran the
-save's device-to-host copy after the delayed restore's host-to-device copy of
-the same slot (both small copies were served in order by one DMA queue), so
-the race it guards against could not be provoked on this platform. The rule
-stays in place because that ordering is not guaranteed.
+every rule in place, so these show those tests would catch a missing wait.
+The reference claims such controls (README.md:114-117) but commits none.
 """
 
 from collections import deque
@@ -163,3 +156,35 @@ def restore_without_victim_wait(gpu):
 
 def test_restore_overwrites_a_victim_before_its_save_without_the_victim_wait(gpu):
     assert shows_race(restore_without_victim_wait, gpu)
+
+
+def save_without_slot_read_wait(gpu):
+    pool = pool_with_bytes(gpu, 3)
+    manager = BlockManager(3, BS)
+    key_a = publish(manager, 0, 5)
+    cache = cache_for(pool, manager, 1, automatic=True, split_streams=True)
+    expected = block(pool, 0)
+    assert cache.save_block(key_a)
+    cache.synchronize()
+    forget(manager, key_a)
+    cache._engine.set_debug(_lib.DEBUG_SKIP_SLOT_READ_WAIT)
+    entry = cache._entries[key_a]
+    manager.free_block_ids = deque([2, 0, 1])
+    delay(cache._restore_stream, gpu)
+    # A prefetch restore (the compute stream does not wait for it) still reading slot 0 ...
+    target = manager.restore_cached_block(key_a, entry.token_ids,
+                                          lambda b: cache._copy_entry(entry, b, wait=False))
+    assert target == 2
+    # ... when its entry is dropped and another block's save reuses the slot.
+    assert cache.discard(key_a)
+    key_b = publish(manager, 1, 6)
+    assert cache.save_block(key_b)
+    assert cache._entries[key_b].slot == entry.slot
+    cache.synchronize()
+    got = block(pool, target)
+    cache.close()
+    return not np.array_equal(got, expected)
+
+
+def test_save_overwrites_a_slot_a_prefetch_still_reads_without_the_slot_read_wait(gpu):
+    assert shows_race(save_without_slot_read_wait, gpu)
