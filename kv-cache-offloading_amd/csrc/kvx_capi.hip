@@ -165,6 +165,27 @@ struct Slab {
   int32_t count;
 };
 
+// Makes the cache's device current for one call and restores the caller's
+// current device afterwards (torch and other callers keep their own notion of
+// the current device; the engine must not change it behind their backs).
+class DeviceScope {
+ public:
+  int enter(int device) {
+    if (hipGetDevice(&prev_) != hipSuccess) prev_ = -1;
+    if (prev_ == device) return KVX_OK;
+    const int rc = hip_status(hipSetDevice(device), "hipSetDevice");
+    changed_ = rc == KVX_OK;
+    return rc;
+  }
+  ~DeviceScope() {
+    if (changed_ && prev_ >= 0) (void)hipSetDevice(prev_);
+  }
+
+ private:
+  int prev_ = -1;
+  bool changed_ = false;
+};
+
 }  // namespace
 
 struct kvx_cache {
@@ -400,7 +421,8 @@ int kvx_cache_create(void* pool, const kvx_block_layout* layout, int32_t format,
   c->split = save_stream != restore_stream;
   c->pending_save.assign(layout->num_blocks, nullptr);
   c->pending_restore.assign(layout->num_blocks, nullptr);
-  rc = hip_status(hipSetDevice(device), "hipSetDevice");
+  DeviceScope scope;
+  rc = scope.enter(device);
   if (!rc) rc = hip_status(hipEventCreateWithFlags(&c->marker, hipEventDisableTiming), "hipEventCreate");
   if (rc) {
     kvx_cache_destroy(c);
@@ -413,7 +435,8 @@ int kvx_cache_create(void* pool, const kvx_block_layout* layout, int32_t format,
 int kvx_cache_destroy(kvx_cache* c) {
   if (!c) return KVX_OK;
   int rc = KVX_OK;
-  (void)hipSetDevice(c->device);
+  DeviceScope scope;
+  (void)scope.enter(c->device);
   if (c->save_stream) rc = hip_status(hipStreamSynchronize(c->save_stream), "hipStreamSynchronize");
   if (c->split && c->restore_stream) {
     int rc2 = hip_status(hipStreamSynchronize(c->restore_stream), "hipStreamSynchronize");
@@ -478,7 +501,8 @@ int kvx_cache_save(kvx_cache* c, const int32_t* ids, const int32_t* slots, int32
   if (!c) return set_error(KVX_E_INVALID, "NULL cache");
   int rc = c->check_lists(ids, slots, n);
   if (rc || n == 0) return rc;
-  rc = hip_status(hipSetDevice(c->device), "hipSetDevice");
+  DeviceScope scope;
+  rc = scope.enter(c->device);
   if (rc) return rc;
   hipStream_t s = c->save_stream;
   // Start after the kernels that wrote these blocks (cpu_prefix_cache.py:310-311).
@@ -522,7 +546,8 @@ int kvx_cache_restore(kvx_cache* c, const int32_t* slots, const int32_t* ids, in
   if (!c) return set_error(KVX_E_INVALID, "NULL cache");
   int rc = c->check_lists(ids, slots, n);
   if (rc || n == 0) return rc;
-  rc = hip_status(hipSetDevice(c->device), "hipSetDevice");
+  DeviceScope scope;
+  rc = scope.enter(c->device);
   if (rc) return rc;
   hipStream_t s = c->restore_stream;
   hipStream_t compute = (hipStream_t)compute_stream;
@@ -612,7 +637,8 @@ int kvx_cache_set_debug(kvx_cache* c, int32_t flags) {
 
 int kvx_cache_synchronize(kvx_cache* c) {
   if (!c) return set_error(KVX_E_INVALID, "NULL cache");
-  int rc = hip_status(hipSetDevice(c->device), "hipSetDevice");
+  DeviceScope scope;
+  int rc = scope.enter(c->device);
   if (!rc) rc = hip_status(hipStreamSynchronize(c->save_stream), "hipStreamSynchronize");
   if (!rc && c->split) rc = hip_status(hipStreamSynchronize(c->restore_stream), "hipStreamSynchronize");
   return rc;

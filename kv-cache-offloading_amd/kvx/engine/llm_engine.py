@@ -186,6 +186,33 @@ class LLMEngine:
     def is_finished(self):
         return self.scheduler.is_finished()
 
+    def generate(self, prompts, sampling_params, use_tqdm: bool = True) -> list[dict]:
+        """Run prompts to completion; outputs in submission order as {"text", "token_ids"} (llm_engine.py:206-234).
+
+        `sampling_params` is one SamplingParams for every prompt or one per prompt.
+        Text needs the engine's tokenizer.
+        """
+        from time import perf_counter
+
+        from tqdm.auto import tqdm
+
+        if not isinstance(sampling_params, list):
+            sampling_params = [sampling_params] * len(prompts)
+        ids = [self.add_request(prompt, sp) for prompt, sp in zip(prompts, sampling_params)]
+        done: dict[int, list[int]] = {}
+        bar = tqdm(total=len(ids), desc="Generating", dynamic_ncols=True, disable=not use_tqdm)
+        while not self.is_finished():
+            started = perf_counter()
+            finished, num_tokens = self.step()
+            rate = abs(num_tokens) / max(perf_counter() - started, 1e-9)
+            bar.set_postfix({"Prefill" if num_tokens > 0 else "Decode": f"{int(rate)}tok/s"})
+            for seq_id, token_ids in finished:
+                done[seq_id] = token_ids
+                bar.update(1)
+        bar.close()
+        decode = self.tokenizer.decode if self.tokenizer is not None else None
+        return [{"text": decode(done[i]) if decode else None, "token_ids": done[i]} for i in ids]
+
 
 def prefill_slot_mapping(seqs, block_size: int) -> list[int]:
     """Pool slot of every scheduled prefill token (model_runner.py:156-166): block_table[pos // BS] * BS + pos % BS."""

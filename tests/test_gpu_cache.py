@@ -264,3 +264,21 @@ def test_measure_restore_time_is_positive(gpu):
     cache = new_cache(pool, BlockManager(2, BS), fp8=True)
     seconds = cache.measure_restore_s_per_block(repeats=4)
     assert 0 < seconds < 1
+
+
+def test_every_split_cache_gets_copy_streams_that_run_concurrently(gpu):
+    # Torch's pool streams map round-robin onto the process's hardware queues; without
+    # the concurrency check every other cache's save and restore streams shared one
+    # queue and ran one after the other.
+    pool = make_pool(gpu, 2)
+    compute = torch.cuda.current_stream(gpu)
+    for _ in range(6):
+        cache = new_cache(pool, BlockManager(2, BS), split_streams=True)
+        engine = cache._engine
+        assert engine.streams_concurrent
+        streams = {engine.save_stream.cuda_stream, engine.restore_stream.cuda_stream, compute.cuda_stream}
+        assert len(streams) == 3
+        cache.close()
+    single = new_cache(pool, BlockManager(2, BS))
+    assert single._engine.streams_concurrent and single._engine.save_stream == single._engine.restore_stream
+    single.close()

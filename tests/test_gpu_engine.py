@@ -269,6 +269,35 @@ def test_preallocated_multi_slab_slots_round_trip_byte_exact(gpu, monkeypatch):
         assert torch.equal(block_bytes(engine, restored), data)
 
 
+@pytest.mark.parametrize("bad_budget", [0, -1, 1.5, True])
+def test_invalid_budget_is_rejected_before_creating_cache(gpu, bad_budget):
+    """bench/test_cpu_prefix_cache.py:255-260."""
+    engine, _, _ = completed_prefix(gpu)
+    with pytest.raises(ValueError, match="positive integer"):
+        engine.create_cpu_prefix_cache(bad_budget)
+    assert engine._cpu_prefix_cache is None
+
+
+def test_tp_and_layout_mismatch_are_rejected(gpu):
+    """bench/test_cpu_prefix_cache.py:263-272."""
+    engine, _, _ = completed_prefix(gpu)
+    engine.model_runner.world_size = 2
+    with pytest.raises(NotImplementedError, match="TP=1"):
+        new_cache(engine)
+    engine.model_runner.world_size = 1
+    engine.model_runner.block_size = 128
+    with pytest.raises(ValueError, match="layout"):
+        new_cache(engine)
+
+
+def test_save_on_release_requires_automatic_mode(gpu):
+    """bench/test_cpu_prefix_cache.py:349-353."""
+    engine, _, _ = completed_prefix(gpu)
+    with pytest.raises(ValueError, match="automatic"):
+        engine.create_cpu_prefix_cache(max_bytes=1 << 20, save_on_release=True)
+    assert engine._cpu_prefix_cache is None
+
+
 # -- bench/test_automatic_cpu_cache.py --------------------------------------------
 
 def automatic_cache(engine, blocks=2, **kwargs):
@@ -355,6 +384,92 @@ def test_full_cpu_budget_falls_back_to_recomputation(gpu):
     assert cache.stats["budget_skips"] >= 1
     assert cache.stats["saved_blocks"] == cache.stats["restored_blocks"] == 0
     assert_pool_consistent(manager)
+
+
+def test_gpu_hits_are_shared_with_active_requests_without_cpu_copy(gpu):
+    """bench/test_automatic_cpu_cache.py:142-155."""
+    engine = cached_engine(gpu, [[10], [20]], budget=512, num_blocks=3)
+    manager = engine.scheduler.block_manager
+    cache = automatic_cache(engine)
+    first_id = engine.add_request([1] * 257, params(max_tokens=3))
+    engine.step_with_events()
+    first = engine.scheduler.running[0]
+    block_id = manager.hash_to_block_id[manager.compute_hash([1] * BS)]
+    engine.add_request([1] * 257 + [10] + [2] * 10, params(max_tokens=1))
+    assert engine.step_with_events().num_tokens == 12
+    assert first.seq_id == first_id and manager.blocks[block_id].ref_count == 1
+    assert cache.stats == {"saved_blocks": 0, "restored_blocks": 0, "budget_skips": 0}
+    assert_pool_consistent(manager)
+
+
+def test_failed_later_admission_keeps_already_prefilled_chunks(gpu, monkeypatch):
+    """bench/test_automatic_cpu_cache.py:290-326."""
+    engine = cached_engine(gpu, [[20], [90], [91], [92], [10], [13, 14]], budget=512, num_blocks=5)
+    manager = engine.scheduler.block_manager
+    engine.add_request([3] * 257, params(max_tokens=1))
+    engine.step_with_events()
+    cache = automatic_cache(engine, blocks=2)
+    key = manager.compute_hash([3] * BS)
+    cache.save_block(key)
+    engine.add_request([9] * 1025, params(max_tokens=1))
+    for _ in range(3):
+        engine.step_with_events()
+    assert key not in manager.hash_to_block_id
+    first_id = engine.add_request([1] * 513, params(max_tokens=1))
+    second_id = engine.add_request([3] * 257, params(max_tokens=1))
+    engine.step_with_events()  # the first request's first 512 tokens are prefilled
+    first = engine.scheduler.waiting[0]
+    blocks = first.block_table.copy()
+    assert first.num_cached_tokens == 512
+
+    def fail(*args, **kwargs):
+        raise RuntimeError("restore failed")
+
+    with monkeypatch.context() as patch:
+        patch.setattr(cache, "_copy_entry", fail)
+        with pytest.raises(RuntimeError, match="restore failed"):
+            engine.step_with_events()
+    assert [seq.seq_id for seq in engine.scheduler.waiting] == [first_id, second_id]
+    assert not engine.scheduler.running
+    assert first.block_table == blocks and first.num_cached_tokens == 512 and first.num_scheduled_tokens == 0
+    assert manager.used_block_ids == set(blocks)
+    assert_pool_consistent(manager)
+    result = engine.step_with_events()
+    assert result.num_tokens == 2
+    assert result.outputs == [(first_id, [13]), (second_id, [14])]
+    assert not manager.used_block_ids
+
+
+def test_cpu_hits_do_not_make_an_oversized_active_request_fit(gpu):
+    """bench/test_automatic_cpu_cache.py:329-340."""
+    engine, manager, key = completed_prefix(gpu, [[90], [91]])
+    cache = automatic_cache(engine, blocks=1)
+    for prompt in ([3] * 257, [4]):
+        engine.add_request(prompt, params(max_tokens=1))
+        engine.step_with_events()
+    assert key in cache and key not in manager.hash_to_block_id
+    seq = Sequence([1] * 513, params(max_tokens=1))
+    before = (list(manager.free_block_ids), cache.stats)
+    assert manager.can_allocate(seq) == -1  # three GPU blocks needed, the pool has two
+    assert (list(manager.free_block_ids), cache.stats) == before
+    assert not seq.block_table
+
+
+def test_repeated_admission_checks_do_not_rehash_a_waiting_prompt(gpu, monkeypatch):
+    """bench/test_automatic_cpu_cache.py:391-404."""
+    engine, manager, key = completed_prefix(gpu, [[90], [91]])
+    cache = automatic_cache(engine, blocks=1)
+    for prompt in ([3] * 257, [4]):
+        engine.add_request(prompt, params(max_tokens=1))
+        engine.step_with_events()
+    assert key in cache and key not in manager.hash_to_block_id
+    seq = Sequence([1] * 257, params(max_tokens=1))
+    assert manager.can_allocate(seq) == 1
+    calls = []
+    original = manager.compute_hash
+    monkeypatch.setattr(manager, "compute_hash", lambda *a: calls.append(a) or original(*a))
+    assert manager.can_allocate(seq) == 1
+    assert calls == []
 
 
 def test_close_detaches_automatic_hooks(gpu):
@@ -670,3 +785,26 @@ def test_later_requests_join_the_step_of_a_split_admission_head(gpu):
     assert engine.step_with_events().num_tokens == 10
     assert engine.is_finished()
     assert_pool_consistent(manager)
+
+
+def test_split_admission_that_recomputes_everything_uses_no_restore(gpu):
+    """bench/test_cpu_cache_optimizations.py:178-189."""
+    engine, manager, keys = finite_prefix(gpu, [[90], [91]], blocks=2, num_blocks=4)
+    pool = pool_of(engine)
+    size = pool[:, :, 0].numel() * pool.element_size()
+    cache = engine.create_cpu_prefix_cache(max_bytes=2 * size, automatic=True)
+    cache.hybrid = (1.0, 0, 0)  # recompute is free
+    drop_gpu_copies(cache, manager, pool, keys)
+    request = engine.add_request([1] * 512 + [5], params(max_tokens=1))
+    engine.step_with_events()
+    seq = next(seq for seq in engine.scheduler.waiting if seq.seq_id == request)
+    assert seq.num_cached_tokens == 512 and seq.restore_span is None  # computed, not skipped
+    assert cache.stats["restored_blocks"] == 0
+
+
+def test_hybrid_requires_automatic_cache(gpu):
+    """bench/test_cpu_cache_optimizations.py:207-211."""
+    engine, _, _ = finite_prefix(gpu)
+    cache = engine.create_cpu_prefix_cache(max_bytes=1 << 20)
+    with pytest.raises(ValueError, match="automatic"):
+        cache.hybrid = (1.0, 0, 0)

@@ -7,6 +7,7 @@ evaluated in numpy.
 """
 
 from dataclasses import replace
+from types import SimpleNamespace
 
 import numpy as np
 import pytest
@@ -17,6 +18,7 @@ from engine_fixtures import cached_engine, params
 from helpers import u8
 from kvx import ops
 from kvx.engine.llm_engine import TokenEvent
+from kvx.engine.sequence import Sequence
 
 pytestmark = pytest.mark.gpu
 
@@ -217,6 +219,42 @@ def test_failed_import_releases_allocated_destination_blocks(gpu, monkeypatch):
         destination.resume_request(snapshot)
     assert destination.is_finished() and not manager.used_block_ids and len(manager.free_block_ids) == 16
     assert request_id in source._detached_requests
+
+
+@pytest.mark.parametrize("sync_fails", [False, True])
+def test_cuda_import_waits_for_readiness_before_admission_and_rolls_back_on_failure(gpu, monkeypatch, sync_fails):
+    """bench/test_engine_handoff.py:198-233: the device sync precedes admission; its failure releases blocks."""
+    source, request_id = prefilled_engine(gpu)
+    snapshot = source.detach_request(request_id)
+    destination = cached_engine(gpu, [])
+    manager = destination.scheduler.block_manager
+    destination.model_runner.kv_cache = SimpleNamespace(device=gpu)
+    imported, synchronized = [], []
+
+    def fake_import(runner, block_manager, snap):
+        seq = Sequence(snap.token_ids[:snap.num_prompt_tokens], params(max_tokens=3))
+        seq.append_token(10)
+        block_manager.allocate_for_resume(seq, snap.num_cached_tokens)
+        imported.append(seq)
+        return seq
+
+    def synchronize(device):
+        assert device == gpu
+        assert not destination.scheduler.running
+        synchronized.append(device)
+        if sync_fails:
+            raise RuntimeError("copy failed")
+
+    monkeypatch.setattr(kv_handoff, "import_kv", fake_import)
+    monkeypatch.setattr(torch.cuda, "synchronize", synchronize)
+    if sync_fails:
+        with pytest.raises(RuntimeError, match="copy failed"):
+            destination.resume_request(snapshot)
+        assert not destination.scheduler.running and not manager.used_block_ids
+    else:
+        assert destination.resume_request(snapshot) == imported[0].seq_id
+        assert list(destination.scheduler.running) == imported
+    assert synchronized == [gpu]
 
 
 def test_exit_releases_detached_source_blocks(gpu):
