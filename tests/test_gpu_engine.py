@@ -402,6 +402,24 @@ def test_gpu_hits_are_shared_with_active_requests_without_cpu_copy(gpu):
     assert_pool_consistent(manager)
 
 
+def test_resume_allocation_failure_releases_partially_reserved_blocks(gpu, monkeypatch):
+    """bench/test_automatic_cpu_cache.py:273-287, with the real cache (tests/test_block_manager.py has a fake)."""
+    engine, manager, _ = completed_prefix(gpu)
+    cache = automatic_cache(engine)
+    seq = Sequence([1] * 257, params(max_tokens=3))
+    seq.append_token(10)
+
+    def fail(*args):
+        raise RuntimeError("preservation failed")
+
+    monkeypatch.setattr(cache, "save_block", fail)
+    with pytest.raises(RuntimeError, match="preservation failed"):
+        manager.allocate_for_resume(seq, 257)
+    assert not seq.block_table and seq.num_cached_tokens == 0
+    assert not manager.used_block_ids
+    assert_pool_consistent(manager)
+
+
 def test_failed_later_admission_keeps_already_prefilled_chunks(gpu, monkeypatch):
     """bench/test_automatic_cpu_cache.py:290-326."""
     engine = cached_engine(gpu, [[20], [90], [91], [92], [10], [13, 14]], budget=512, num_blocks=5)
