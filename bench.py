@@ -53,6 +53,8 @@ def parse_args():
     p.add_argument("--skip-store", action="store_true", help="skip the store_kvcache leg")
     p.add_argument("--skip-hybrid", action="store_true", help="skip the hybrid-admission calibration leg")
     p.add_argument("--skip-agents", action="store_true", help="skip the agent-pressure leg")
+    p.add_argument("--skip-reference-gpu", action="store_true",
+                   help="skip timing the reference's torch codec chain on the GPU")
     p.add_argument("--skip-configs", action="store_true",
                    help="skip the Qwen3-0.6B FP8 and Qwen3-8B BF16 legs")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample budget")
@@ -242,6 +244,41 @@ def timed_pair(torch, first, second, reps=10):
         t1.append(ev[0].elapsed_time(ev[1]) / 1000)
         t2.append(ev[1].elapsed_time(ev[2]) / 1000)
     return sorted(t1)[reps // 2], sorted(t2)[reps // 2]
+
+
+def reference_gpu_leg(torch, pool, sources, dests, scale_dtype, kvx_step_ms, reps=3):
+    """The reference's own implementation of this path, run on this GPU for comparison.
+
+    Per block, the reference quantises into device staging with four torch
+    calls (fp8_quantize, cpu_prefix_cache.py:20-24, via _quantize :225-231)
+    and dequantises into the pool with two (fp8_dequantize :27-28, via
+    _dequantize :236-243). Here the same calls run over the same 128 + 128
+    blocks with every entry staged in HBM (no host copies), exactly the work
+    the kvx step times.
+    """
+    _, layers, _, bs, heads, hd = pool.shape
+    block = (2, layers, bs, heads, hd)
+    n = len(sources)
+    payload = torch.empty((n, *block), dtype=torch.float8_e4m3fn, device=pool.device)
+    scale = torch.empty((n, *block[:-1], 1), dtype=scale_dtype, device=pool.device)
+
+    def save():
+        for i, b in enumerate(sources):
+            source = pool[:, :, b]
+            row_max = source.abs().amax(-1, keepdim=True).float()
+            scale[i].copy_((row_max / 448.0).clamp_min(1e-30))
+            payload[i].copy_((source.float() / scale[i].float()).clamp_(-448.0, 448.0))
+
+    def restore():
+        for i, d in enumerate(dests):
+            torch.mul(payload[i].to(pool.dtype), scale[i], out=pool[:, :, d])
+
+    save_s, restore_s = timed_pair(torch, save, restore, reps=reps)
+    step_ms = 1000 * (save_s + restore_s)
+    return {"blocks_saved": n, "blocks_restored": len(dests), "save_ms": round(1000 * save_s, 3),
+            "restore_ms": round(1000 * restore_s, 3), "step_ms": round(step_ms, 3),
+            "logical_kv_gbs": round(2 * n * BF16_BLOCK_BYTES / (step_ms / 1000) / 1e9, 1),
+            "kvx_speedup": round(step_ms / kvx_step_ms, 2)}
 
 
 def bf16_leg(torch, ops, pool, reps):
@@ -542,6 +579,9 @@ def main():
         log("host link leg")
         result["host_link"] = host_link_leg(torch, pool, ops.pool_layout(pool, scale_dtype), sources, dests,
                                             args.host_reps)
+    if not args.skip_reference_gpu:
+        log("reference torch codec on the GPU")
+        result["reference_torch_gpu"] = reference_gpu_leg(torch, pool, sources, dests, scale_dtype, ms_per_step)
     if not args.skip_configs:
         log("bf16 leg")
         result["bf16_qwen3_8b"] = bf16_leg(torch, ops, pool, args.host_reps)
