@@ -229,7 +229,7 @@ class CPUBlockCache:
         self._saved_blocks = 0
         self._restored_blocks = 0
         self._budget_skips = 0
-        self._layout = ops.pool_layout(cache, scale_dtype)
+        self._layout = ops.pool_layout(cache, scale_dtype if fp8 else None)
         fmt = ops.FORMAT_FP8 if fp8 else ops.FORMAT_RAW
         self._engine = _CopyEngine(cache, self._layout, fmt, split_streams)
         assert self._engine.logical_bytes == self._block_bytes
@@ -374,7 +374,7 @@ class CPUBlockCache:
         self._require_open()
         device = self._cache.device
         scratch = torch.empty((2, self._shape[1], 1, *self._shape[2:]), dtype=self._cache.dtype, device=device)
-        layout = ops.pool_layout(scratch, self._scale_dtype)
+        layout = ops.pool_layout(scratch, self._scale_dtype if self._fp8 else None)
         engine = _CopyEngine(scratch, layout, ops.FORMAT_FP8 if self._fp8 else ops.FORMAT_RAW, False)
         try:
             host = torch.zeros(repeats * engine.entry_stride, dtype=torch.uint8, pin_memory=True)

@@ -156,6 +156,10 @@ def pool_layout(pool: torch.Tensor, scale_dtype: torch.dtype | None = None) -> B
     if pool.ndim != 6 or pool.shape[0] != 2 or not pool.is_contiguous():
         raise ValueError("pool must be a contiguous [2, layers, blocks, block_size, heads, head_dim] tensor")
     _, layers, nb, bs, heads, hd = pool.shape
+    if scale_dtype is not None and scale_dtype not in SCALE_DTYPES:
+        raise ValueError(f"FP8 scales must be bfloat16 or float32, not {scale_dtype}")
+    # Without an explicit scale dtype, scales follow the pool dtype (the reference's default); pools of other
+    # dtypes only use RAW entries, which carry no scales.
     scale = SCALE_DTYPES.get(scale_dtype if scale_dtype is not None else pool.dtype, _lib.SCALE_BF16)
     return BlockLayout(nb * bs * heads * hd, bs * heads * hd, 2 * layers, bs * heads, hd, nb,
                        pool.element_size(), scale)

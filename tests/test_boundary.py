@@ -123,3 +123,14 @@ def test_cache_constructor_validates_like_the_reference():
     runner.world_size, runner.block_size = 1, 128
     with pytest.raises(ValueError, match="layout"):
         CPUBlockCache(runner, manager, 1 << 20)
+
+
+def test_pool_layout_rejects_unsupported_scale_dtypes():
+    pool = torch.zeros((2, 2, 3, 4, 1, 8), dtype=torch.bfloat16)
+    assert ops.pool_layout(pool).scale_dtype == _lib.SCALE_BF16
+    assert ops.pool_layout(pool, torch.float32).scale_dtype == _lib.SCALE_FP32
+    for bad in (torch.float16, torch.float8_e4m3fn, torch.int32):
+        with pytest.raises(ValueError, match="bfloat16 or float32"):
+            ops.pool_layout(pool, bad)
+    raw = ops.pool_layout(pool.to(torch.float16))  # RAW-only pools keep a placeholder scale dtype
+    assert (raw.planes, raw.plane_rows, raw.head_dim, raw.num_blocks) == (4, 4, 8, 3)

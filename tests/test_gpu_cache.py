@@ -282,3 +282,27 @@ def test_every_split_cache_gets_copy_streams_that_run_concurrently(gpu):
     single = new_cache(pool, BlockManager(2, BS))
     assert single._engine.streams_concurrent and single._engine.save_stream == single._engine.restore_stream
     single.close()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_byte_copy_mode_round_trips_pools_of_other_dtypes(gpu, dtype):
+    # BF16 storage mode is a byte copy (cpu_prefix_cache.py:319, 386), so any pool dtype works; FP8 needs bf16.
+    pool = torch.empty((2, 2, 3, BS, 1, 4), dtype=dtype, device=gpu)
+    raw = torch.arange(pool.numel() * pool.element_size(), device=gpu).remainder(256).to(torch.uint8)
+    pool.view(torch.uint8).copy_(raw.view(pool.view(torch.uint8).shape))
+    manager = BlockManager(3, BS)
+    keys = [publish(manager, b, b + 1) for b in (0, 2)]
+    expected = {k: block_bytes(pool, b) for k, b in zip(keys, (0, 2))}
+    cache = new_cache(pool, manager, blocks=2)
+    assert cache.block_bytes == pool[:, :, 0].numel() * pool.element_size()
+    for k in keys:
+        assert cache.save_block(k)
+    cache.synchronize()
+    for k in keys:
+        manager.hash_to_block_id.pop(k)
+    pool.fill_(0)
+    for k in keys:
+        assert np.array_equal(block_bytes(pool, cache.restore_block(k)), expected[k])
+    cache.close()
+    with pytest.raises(NotImplementedError, match="bfloat16 pool"):
+        new_cache(pool, BlockManager(3, BS), fp8=True)
