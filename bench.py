@@ -281,6 +281,70 @@ def reference_gpu_leg(torch, pool, sources, dests, scale_dtype, kvx_step_ms, rep
             "kvx_speedup": round(step_ms / kvx_step_ms, 2)}
 
 
+def reference_link_leg(torch, pool, sources, dests, scale_dtype, reps=3):
+    """The reference's host path for FP8 blocks, run on this GPU for comparison with the host-link leg.
+
+    Per block, a save quantises into the stream's one device staging pair and
+    queues two non-blocking D2H copies (payload, scales) on the copy stream
+    (cpu_prefix_cache.py:225-234, 306-322); a restore copies both back into
+    staging and dequantises into the pool (:236-243, 374-393). Save and
+    restore streams are chosen like the kvx cache's (concurrent queues), so
+    only the implementation differs. Returns link GB/s of logical entry bytes.
+    """
+    from kvx.engine.cpu_prefix_cache import _copy_streams
+
+    (save_stream, restore_stream), _ = _copy_streams(pool.device, 2)
+    _, layers, _, bs, heads, hd = pool.shape
+    block, rows = (2, layers, bs, heads, hd), (2, layers, bs, heads, 1)
+    n = len(sources)
+    host_payload = torch.empty((2 * n, *block), dtype=torch.float8_e4m3fn, pin_memory=True)
+    host_scale = torch.empty((2 * n, *rows), dtype=scale_dtype, pin_memory=True)
+    stage = [(torch.empty(block, dtype=torch.float8_e4m3fn, device=pool.device),
+              torch.empty(rows, dtype=scale_dtype, device=pool.device)) for _ in range(2)]
+
+    def quantize(source, payload, scale):
+        row_max = source.abs().amax(-1, keepdim=True).float()
+        scale.copy_((row_max / 448.0).clamp_min(1e-30))
+        payload.copy_((source.float() / scale.float()).clamp_(-448.0, 448.0))
+
+    def save(first):
+        payload, scale = stage[0]
+        with torch.cuda.stream(save_stream):
+            for i, b in enumerate(sources):
+                quantize(pool[:, :, b], payload, scale)
+                host_payload[first + i].copy_(payload, non_blocking=True)
+                host_scale[first + i].copy_(scale, non_blocking=True)
+
+    def restore():
+        payload, scale = stage[1]
+        with torch.cuda.stream(restore_stream):
+            for i, d in enumerate(dests):
+                payload.copy_(host_payload[i], non_blocking=True)
+                scale.copy_(host_scale[i], non_blocking=True)
+                torch.mul(payload.to(pool.dtype), scale, out=pool[:, :, d])
+
+    def timed(*fns):
+        best = None
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for fn in fns:
+                fn()
+            torch.cuda.synchronize()
+            dt = time.perf_counter() - t0
+            best = dt if best is None else min(best, dt)
+        return best
+
+    save(0)  # entries for the restores to read
+    torch.cuda.synchronize()
+    link = n * (host_payload[0].numel() + host_scale[0].numel() * host_scale.element_size())
+    save_s = timed(lambda: save(n))
+    restore_s = timed(restore)
+    both_s = timed(lambda: save(n), restore)
+    return {"bytes_per_direction": link, "save_d2h_gbs": round(link / save_s / 1e9, 2),
+            "restore_h2d_gbs": round(link / restore_s / 1e9, 2), "duplex_gbs": round(2 * link / both_s / 1e9, 2)}
+
+
 def bf16_leg(torch, ops, pool, reps):
     """BF16 storage mode on the Qwen3-8B pool: byte gather of 200 seeded blocks into entries and scatter into a
     seeded permutation of the pool (HBM-resident), then 128 + 128 blocks over the host link."""
@@ -582,6 +646,9 @@ def main():
     if not args.skip_reference_gpu:
         log("reference torch codec on the GPU")
         result["reference_torch_gpu"] = reference_gpu_leg(torch, pool, sources, dests, scale_dtype, ms_per_step)
+        if not args.skip_host_link:
+            log("reference host path on the GPU")
+            result["reference_torch_gpu"]["host_link"] = reference_link_leg(torch, pool, sources, dests, scale_dtype)
     if not args.skip_configs:
         log("bf16 leg")
         result["bf16_qwen3_8b"] = bf16_leg(torch, ops, pool, args.host_reps)
