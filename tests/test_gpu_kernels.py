@@ -298,3 +298,47 @@ def test_store_kvcache_replays_inside_a_hip_graph(gpu):
         oracle.store_kvcache(bf16_bits(key), bf16_bits(value), expect_k, expect_v, slots)
         assert np.array_equal(bf16_bits(pool[0, 0]).reshape(slots_total, -1), expect_k), step
         assert np.array_equal(bf16_bits(pool[1, 0]).reshape(slots_total, -1), expect_v), step
+
+
+@pytest.mark.parametrize("scale_dtype", [torch.float32, torch.bfloat16])
+def test_fp8_block_save_and_restore_replay_inside_a_hip_graph(gpu, scale_dtype):
+    # Block lists travel in the kernel arguments, so a captured save + restore
+    # replays with no host work; each replay must match the eager result.
+    pool = make_pool(gpu, layers=3, blocks=6)
+    layout = ops.pool_layout(pool, scale_dtype)
+    _, offset, stride = ops.entry_layout(layout, ops.FORMAT_FP8)
+    sources, dests = [4, 1], [0, 5]
+    staging = torch.zeros(len(sources) * stride, dtype=torch.uint8, device=gpu)
+    entries = [staging.data_ptr() + i * stride for i in range(len(sources))]
+
+    def step():
+        ops.save_blocks(pool, sources, entries, ops.FORMAT_FP8, scale_dtype)
+        ops.restore_blocks(pool, dests, entries, ops.FORMAT_FP8, scale_dtype)
+
+    stream = torch.cuda.Stream(gpu)
+    stream.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(stream):
+        step()  # warm-up outside capture
+    torch.cuda.current_stream(gpu).wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    g = torch.Generator(device=gpu).manual_seed(3)
+    for replay in range(4):
+        fresh = torch.randn(pool[:, :, sources].shape, generator=g, device=gpu) * (replay + 1)
+        pool[:, :, sources] = fresh.to(torch.bfloat16)  # eager work between replays
+        torch.cuda.synchronize()
+        before = pool.clone()
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed, replayed_entries = pool.clone(), staging.clone()
+        pool.copy_(before)
+        step()
+        torch.cuda.synchronize()
+        assert torch.equal(replayed.view(torch.int16), pool.view(torch.int16)), replay
+        assert torch.equal(replayed_entries, staging), replay
+        host_pool = bf16_bits(before)
+        for b, d in zip(sources, dests):
+            codes, scales = oracle.save_block_fp8(host_pool, b, scale_dtype == torch.float32)
+            expect = oracle.dequantize(codes, scales, scale_dtype == torch.float32)
+            assert np.array_equal(bf16_bits(replayed[:, :, d]), expect), (replay, b)
