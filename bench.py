@@ -438,6 +438,27 @@ def host_link_leg(torch, pool, layout, sources, dests, reps, fmt=None, ceilings=
 
         both_s = timed(both)
 
+        # What CPUBlockCache does: one engine call per block, with its default staging.
+        from kvx.engine.cpu_prefix_cache import _MAX_BATCH, _STAGING_BYTES
+
+        engine.set_staging(save_staging, restore_staging, max(1, min(_MAX_BATCH, _STAGING_BYTES // stride)))
+
+        def save_each():
+            for b, slot in zip(sources, high):
+                engine.save([b], [slot], compute)
+
+        def restore_each():
+            for slot, d in zip(low, dests):
+                engine.restore([slot], [d], False, compute)
+
+        def both_each():
+            for b, s_slot, r_slot, d in zip(sources, high, low, dests):
+                engine.save([b], [s_slot], compute)
+                engine.restore([r_slot], [d], False, compute)
+
+        each_save_s, each_restore_s, each_both_s = timed(save_each), timed(restore_each), timed(both_each)
+        engine.set_staging(save_staging, restore_staging, n)
+
         ceil_d2h = ceil_h2d = ceil_both = None
         if ceilings:
             # Ceiling: pinned hipMemcpyAsync each way, and both at once on the
@@ -486,6 +507,9 @@ def host_link_leg(torch, pool, layout, sources, dests, reps, fmt=None, ceilings=
             "pin_seconds": round(pin_s, 2),
             "logical_kv_gbs": round(2 * n * BF16_BLOCK_BYTES / both_s / 1e9, 2),
             "streams_concurrent": engine.streams_concurrent,
+            "per_block_calls": {"save_d2h_gbs": round(gbs(link_bytes, each_save_s), 2),
+                                "restore_h2d_gbs": round(gbs(link_bytes, each_restore_s), 2),
+                                "duplex_gbs": round(gbs(2 * link_bytes, each_both_s), 2)},
         }
         if ceilings:
             out.update({

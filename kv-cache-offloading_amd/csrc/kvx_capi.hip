@@ -277,6 +277,16 @@ struct kvx_cache {
     return KVX_OK;
   }
 
+  // Saves of at most this many entry bytes per call write the pinned slots
+  // straight from the save kernel instead of staging + D2H DMA. On MI355X a
+  // D2H DMA queued behind a kernel that itself waited for another stream's
+  // event started ~0.65 ms late; one such wait per call is paid by every save
+  // call, so one-block saves (the block manager's pattern) ran at 31-40 GB/s
+  // staged against 49 GB/s written by the kernel, and a save + restore stream
+  // pair at 28 against 60 GB/s. Larger calls amortise the wait and keep the
+  // DMA (55 GB/s).
+  static constexpr int64_t kDirectSaveBytes = 256ll << 20;
+
   // Copies `count` entries between consecutive staging entries and host
   // slots. Runs of consecutive slots in one slab are merged, then cut into
   // pieces of at most kDmaPiece bytes: two multi-gigabyte copies queued at the
@@ -312,12 +322,16 @@ struct kvx_cache {
     return scale_offset + rows * (layout.scale_dtype == KVX_SCALE_BF16 ? 2 : 4);
   }
 
-  int launch(bool save, const int32_t* ids, uint8_t* staging, int32_t count, hipStream_t s) {
+  // Launches the save or restore kernel for `count` (<= kMaxBatch) blocks whose
+  // entries start at staging (consecutive entries) or, with staging == nullptr,
+  // at the host slots `slots` (the kernel then moves the bytes over the host link).
+  int launch(bool save, const int32_t* ids, uint8_t* staging, const int32_t* slots, int32_t count,
+             hipStream_t s) {
     BlockBatch b;
     b.n = count;
     for (int32_t i = 0; i < count; ++i) {
       b.ids[i] = ids[i];
-      b.entries[i] = (uint64_t)(uintptr_t)(staging + (int64_t)i * entry_stride);
+      b.entries[i] = (uint64_t)(uintptr_t)(staging ? staging + (int64_t)i * entry_stride : host_entry(slots[i]));
     }
     const bool vec = vector_access_ok(pool, layout, b.entries, b.n);
     hipError_t err = save ? launch_save(pool, layout, format, b, scale_offset, vec, s)
@@ -519,12 +533,19 @@ int kvx_cache_save(kvx_cache* c, const int32_t* ids, const int32_t* slots, int32
       }
     }
   }
-  const int32_t step = c->chunk();
-  for (int32_t base = 0; base < n; base += step) {
-    const int32_t cnt = std::min(step, n - base);
-    rc = c->launch(true, ids + base, c->save_staging, cnt, s);
-    if (!rc) rc = c->dma(true, c->save_staging, slots + base, cnt, s);
-    if (rc) return rc;
+  if ((int64_t)n * c->logical_bytes_with_scales() <= kvx_cache::kDirectSaveBytes) {
+    for (int32_t base = 0; base < n; base += kMaxBatch) {
+      rc = c->launch(true, ids + base, nullptr, slots + base, std::min(kMaxBatch, n - base), s);
+      if (rc) return rc;
+    }
+  } else {
+    const int32_t step = c->chunk();
+    for (int32_t base = 0; base < n; base += step) {
+      const int32_t cnt = std::min(step, n - base);
+      rc = c->launch(true, ids + base, c->save_staging, nullptr, cnt, s);
+      if (!rc) rc = c->dma(true, c->save_staging, slots + base, cnt, s);
+      if (rc) return rc;
+    }
   }
   Event* done = nullptr;
   rc = c->new_event(&done);
@@ -574,7 +595,7 @@ int kvx_cache_restore(kvx_cache* c, const int32_t* slots, const int32_t* ids, in
   for (int32_t base = 0; base < n; base += step) {
     const int32_t cnt = std::min(step, n - base);
     rc = c->dma(false, c->restore_staging, slots + base, cnt, s);
-    if (!rc) rc = c->launch(false, ids + base, c->restore_staging, cnt, s);
+    if (!rc) rc = c->launch(false, ids + base, c->restore_staging, nullptr, cnt, s);
     if (rc) return rc;
   }
   Event* done = nullptr;
