@@ -533,6 +533,16 @@ int kvx_cache_save(kvx_cache* c, const int32_t* ids, const int32_t* slots, int32
       }
     }
   }
+  // After a background restore still writing a source block (a prefetched
+  // block whose CPU entry was dropped can be saved again before first use).
+  if (c->split) {
+    for (int32_t i = 0; i < n; ++i) {
+      if (Event* pr = c->pending_restore[ids[i]]) {
+        rc = c->wait_event(s, pr);
+        if (rc) return rc;
+      }
+    }
+  }
   if ((int64_t)n * c->logical_bytes_with_scales() <= kvx_cache::kDirectSaveBytes) {
     for (int32_t base = 0; base < n; base += kMaxBatch) {
       rc = c->launch(true, ids + base, nullptr, slots + base, std::min(kMaxBatch, n - base), s);

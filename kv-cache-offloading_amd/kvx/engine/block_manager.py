@@ -9,6 +9,7 @@ duck-typed hooks) plugs in unchanged.
 """
 
 from collections import deque
+from contextlib import nullcontext
 from collections.abc import Callable, Sequence as TokenSequence
 
 import numpy as np
@@ -202,6 +203,11 @@ class BlockManager:
             memo.append((h, token_ids, tuple(token_ids)))
         return memo
 
+    def _batched_copies(self):
+        """The cache's coalesce() context (restores handed over as batches), if it has one."""
+        coalesce = getattr(self._cpu_prefix_cache, "coalesce", None)
+        return coalesce() if coalesce is not None else nullcontext()
+
     def prefetch(self, seq: Sequence, reserve: int = 0) -> int:
         """Start background restores of a waiting request's CPU hits (:202-237); returns how many.
 
@@ -227,15 +233,16 @@ class BlockManager:
             self.free_block_ids.append(block_id)
         self._protected = set(own_idle)
         started = 0
-        for h, token_ids, block_id, entry in prefix:
-            if started == budget:
-                break
-            if entry is None:
-                continue
-            target = self.restore_cached_block(
-                h, token_ids, lambda target, e=entry: cache._copy_entry(e, target, wait=False))
-            self._protected.add(target)
-            started += 1
+        with self._batched_copies():
+            for h, token_ids, block_id, entry in prefix:
+                if started == budget:
+                    break
+                if entry is None:
+                    continue
+                target = self.restore_cached_block(
+                    h, token_ids, lambda target, e=entry: cache._copy_entry(e, target, wait=False))
+                self._protected.add(target)
+                started += 1
         cache._prefetched_blocks += started
         return started
 
@@ -296,20 +303,21 @@ class BlockManager:
                     self._acquire_block(block_id)
                     owned.append(block_id)
                     table[i] = block_id
-            for i, (h, token_ids, block_id, entry) in enumerate(prefix):
-                if block_id is not None or i < split:
-                    continue
-                block_id = self._allocate_block()
-                owned.append(block_id)
-                table[i] = block_id
-                # After a split, the head's prefill overlaps these copies and
-                # finish_restore_span orders the first read after them.
-                if split:
-                    self._cpu_prefix_cache._copy_entry(entry, block_id, wait=False)
-                else:
-                    self._cpu_prefix_cache._copy_entry(entry, block_id)
-                self.blocks[block_id].update(h, token_ids)
-                self.hash_to_block_id[h] = block_id
+            with self._batched_copies():
+                for i, (h, token_ids, block_id, entry) in enumerate(prefix):
+                    if block_id is not None or i < split:
+                        continue
+                    block_id = self._allocate_block()
+                    owned.append(block_id)
+                    table[i] = block_id
+                    # After a split, the head's prefill overlaps these copies and
+                    # finish_restore_span orders the first read after them.
+                    if split:
+                        self._cpu_prefix_cache._copy_entry(entry, block_id, wait=False)
+                    else:
+                        self._cpu_prefix_cache._copy_entry(entry, block_id)
+                    self.blocks[block_id].update(h, token_ids)
+                    self.hash_to_block_id[h] = block_id
             for i in [*range(split), *range(num_cached_blocks, seq.num_blocks)]:
                 block_id = self._allocate_block()
                 owned.append(block_id)

@@ -17,6 +17,7 @@ torch-op path for CPU-resident pools.
 """
 
 import ctypes
+from contextlib import contextmanager
 from dataclasses import dataclass
 from math import prod
 
@@ -236,6 +237,10 @@ class CPUBlockCache:
         self._copy_stream = self._engine.save_stream
         self._restore_stream = self._engine.restore_stream
         self._staging: list[torch.Tensor] = []
+        self._coalescing = 0  # depth of coalesce() blocks
+        self._queued: list[tuple[int, int, bool]] = []  # (slot, block, wait) restores held back
+        self._queued_blocks: set[int] = set()
+        self._queued_slots: set[int] = set()
         if automatic:
             if block_manager._cpu_prefix_cache is not None:
                 self._engine.close()
@@ -399,17 +404,59 @@ class CPUBlockCache:
     def synchronize(self):
         """Wait for every pending host<->device copy (needed before host reads)."""
         if not self.closed:
+            self._flush()
             self._engine.synchronize()
 
     def _save_to_slot(self, block_id: int, slot: int):
         """Queue pool block -> host slot on the save stream (the seam failure-injection tests patch)."""
         self._ensure_staging()
+        if block_id in self._queued_blocks or slot in self._queued_slots:
+            self._flush()
         self._engine.save([block_id], [slot], self._compute_stream())
 
     def _restore_from_slot(self, slot: int, block_id: int, wait: bool):
-        """Queue host slot -> pool block on the restore stream."""
+        """Queue host slot -> pool block on the restore stream (held back inside coalesce())."""
         self._ensure_staging()
+        if self._coalescing:
+            self._queued.append((slot, block_id, wait))
+            self._queued_blocks.add(block_id)
+            self._queued_slots.add(slot)
+            return
         self._engine.restore([slot], [block_id], wait, self._compute_stream())
+
+    @contextmanager
+    def coalesce(self):
+        """Hand the restores issued inside the block to the copy engine as batched calls on exit.
+
+        One engine call per block costs a cross-stream wait per block: on
+        MI355X one-block restores ran at ~47 GB/s against ~55 GB/s for a batch.
+        Restores with wait=True make the caller's stream wait at the end of the
+        block instead of after each restore, so no work that reads a restored
+        block may be queued on that stream inside it. Anything that touches a
+        queued block or slot (a save, before_block_use/reuse, synchronize)
+        flushes the queue first. The block manager's admission and prefetch
+        loops use this.
+        """
+        self._coalescing += 1
+        try:
+            yield
+        finally:
+            self._coalescing -= 1
+            if not self._coalescing:
+                self._flush()
+
+    def _flush(self):
+        queued, self._queued = self._queued, []
+        self._queued_blocks, self._queued_slots = set(), set()
+        start = 0
+        while start < len(queued):
+            end, wait = start, queued[start][2]
+            while end < len(queued) and queued[end][2] == wait:
+                end += 1
+            run = queued[start:end]
+            self._engine.restore([slot for slot, _, _ in run], [block for _, block, _ in run], wait,
+                                 self._compute_stream())
+            start = end
 
     def save_block(self, prefix_hash: int) -> bool:
         """Save a published full block; return False if already saved (cpu_prefix_cache.py:275-332).
@@ -467,10 +514,14 @@ class CPUBlockCache:
 
     def before_block_reuse(self, block_id: int):
         """Order later writes to a GPU block after its pending save and restore, without a host sync."""
+        if block_id in self._queued_blocks:
+            self._flush()
         self._engine.before_block_reuse(block_id, self._compute_stream())
 
     def before_block_use(self, block_id: int):
         """Order later reads of a prefetched GPU block after its restore."""
+        if block_id in self._queued_blocks:
+            self._flush()
         self._engine.before_block_use(block_id, self._compute_stream())
 
     def _entry_for(self, prefix_hash: int, token_ids):

@@ -9,6 +9,7 @@ stream before each copy (test_automatic_cpu_cache.py:37-51) and pinned slabs
 poisoned with 0xAB (test_cpu_cache_optimizations.py:83-86).
 """
 
+from collections import deque
 from types import SimpleNamespace
 
 import numpy as np
@@ -306,3 +307,66 @@ def test_byte_copy_mode_round_trips_pools_of_other_dtypes(gpu, dtype):
     cache.close()
     with pytest.raises(NotImplementedError, match="bfloat16 pool"):
         new_cache(pool, BlockManager(3, BS), fp8=True)
+
+
+def test_save_of_a_block_waits_for_its_pending_restore(gpu):
+    # A prefetched block whose CPU entry was dropped can be saved again before
+    # its first use; the save must read the restored bytes, not the old ones.
+    pool = make_pool(gpu, 3)
+    manager = BlockManager(3, BS)
+    key = publish(manager, 0, 1)
+    cache = new_cache(pool, manager, blocks=2, split_streams=True)
+    expected = block_bytes(pool, 0)
+    assert cache.save_block(key)
+    cache.synchronize()
+    forget(manager, key)
+    pool[:, :, 2].fill_(0)
+    manager.free_block_ids = deque([2, 0, 1])
+    entry = cache._entries[key]
+    ops.sleep(DELAY_US, stream=cache._restore_stream, device=gpu)
+    target = manager.restore_cached_block(key, entry.token_ids, lambda b: cache._copy_entry(entry, b, wait=False))
+    assert target == 2
+    assert cache.discard(key)
+    cache._free_slots.remove(entry.slot)  # the new save takes the other slot, so only the new rule orders it
+    cache._free_slots.insert(0, entry.slot)
+    assert cache.save_block(key)
+    assert cache._entries[key].slot != entry.slot
+    cache.synchronize()
+    assert np.array_equal(u8(cache._entries[key].kv), expected)
+    assert np.array_equal(block_bytes(pool, 2), expected)
+    cache.close()
+
+
+def test_coalesced_restores_land_before_dependent_work(gpu):
+    pool = make_pool(gpu, 6)
+    manager = BlockManager(6, BS)
+    keys = [publish(manager, b, 20 + b) for b in range(3)]
+    expected = {k: block_bytes(pool, b) for b, k in enumerate(keys)}
+    cache = new_cache(pool, manager, blocks=3, split_streams=True)
+    for k in keys:
+        assert cache.save_block(k)
+    cache.synchronize()
+    for k in keys:
+        forget(manager, k)
+    pool.fill_(0)
+    slow_copies(cache)
+    entries = [cache._entries[k] for k in keys]
+    with cache.coalesce():
+        cache._copy_entry(entries[0], 3)  # wait=True: compute waits when the block ends
+        cache._copy_entry(entries[1], 4, wait=False)
+        assert len(cache._queued) == 2  # held back
+        # A save of a queued block flushes first and reads the restored bytes.
+        manager.blocks[4].update(keys[1], [21] * BS)
+        manager.hash_to_block_id[keys[1]] = 4
+        cache.discard(keys[1])
+        assert cache.save_block(keys[1]) and not cache._queued
+        cache._copy_entry(entries[2], 5, wait=False)
+    assert not cache._queued
+    copy = pool[:, :, 3].clone()  # compute-stream work after the block sees the restored bytes
+    cache.before_block_use(5)
+    copy5 = pool[:, :, 5].clone()
+    cache.synchronize()
+    assert np.array_equal(u8(copy), expected[keys[0]])
+    assert np.array_equal(u8(copy5), expected[keys[2]])
+    assert np.array_equal(u8(cache._entries[keys[1]].kv), expected[keys[1]])
+    cache.close()
