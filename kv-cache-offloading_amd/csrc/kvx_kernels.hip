@@ -27,7 +27,6 @@ constexpr float kScaleFloor = 1e-30f;
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------
@@ -42,10 +41,6 @@ __device__ __forceinline__ uint4 load_nt16(const void* p) {
 __device__ __forceinline__ void store_nt16(void* p, uint4 v) {
   u32x4 w = {v.x, v.y, v.z, v.w};
   __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(p));
-}
-__device__ __forceinline__ void store_nt8(void* p, uint2 v) {
-  u32x2 w = {v.x, v.y};
-  __builtin_nontemporal_store(w, reinterpret_cast<u32x2*>(p));
 }
 
 // Workgroups are dispatched round-robin over the chip's 8 XCDs, each with its
