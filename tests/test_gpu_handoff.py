@@ -15,7 +15,6 @@ import torch
 
 import kvx.engine.kv_handoff as kv_handoff
 from engine_fixtures import cached_engine, params
-from helpers import u8
 from kvx import ops
 from kvx.engine.llm_engine import TokenEvent
 from kvx.engine.sequence import Sequence
