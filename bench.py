@@ -345,7 +345,7 @@ def reference_link_leg(torch, pool, sources, dests, scale_dtype, reps=3):
             "restore_h2d_gbs": round(link / restore_s / 1e9, 2), "duplex_gbs": round(2 * link / both_s / 1e9, 2)}
 
 
-def bf16_leg(torch, ops, pool, reps):
+def bf16_leg(torch, ops, pool, reps, link=True):
     """BF16 storage mode on the Qwen3-8B pool: byte gather of 200 seeded blocks into entries and scatter into a
     seeded permutation of the pool (HBM-resident), then 128 + 128 blocks over the host link."""
     from kvx.workloads import block_selection
@@ -362,7 +362,8 @@ def bf16_leg(torch, ops, pool, reps):
     del staging
     moved = len(sources) * 2 * BF16_BLOCK_BYTES  # read + written per launch
     order = block_selection(nb, 256, seed=1)
-    link = host_link_leg(torch, pool, layout, order[:128], order[128:], reps, fmt=ops.FORMAT_RAW, ceilings=False)
+    link = host_link_leg(torch, pool, layout, order[:128], order[128:], reps, fmt=ops.FORMAT_RAW,
+                         ceilings=False) if link else None
     return {"blocks": len(sources), "algorithmic_bytes_per_launch": moved,
             "gather": {"ms": round(1000 * gather_s, 4), "hbm_gbs": round(moved / gather_s / 1e9, 1),
                        "frac": round(moved / gather_s / 1e9 / HBM_PEAK_GBS, 4)},
@@ -675,7 +676,7 @@ def main():
             result["reference_torch_gpu"]["host_link"] = reference_link_leg(torch, pool, sources, dests, scale_dtype)
     if not args.skip_configs:
         log("bf16 leg")
-        result["bf16_qwen3_8b"] = bf16_leg(torch, ops, pool, args.host_reps)
+        result["bf16_qwen3_8b"] = bf16_leg(torch, ops, pool, args.host_reps, link=not args.skip_host_link)
         log("qwen3-0.6b leg")
         result["fp8_qwen3_0_6b"] = qwen3_0_6b_leg(torch, ops, scale_dtype)
     if not args.skip_hybrid:
