@@ -134,3 +134,14 @@ def test_pool_layout_rejects_unsupported_scale_dtypes():
             ops.pool_layout(pool, bad)
     raw = ops.pool_layout(pool.to(torch.float16))  # RAW-only pools keep a placeholder scale dtype
     assert (raw.planes, raw.plane_rows, raw.head_dim, raw.num_blocks) == (4, 4, 8, 3)
+
+
+def test_a_missing_library_fails_loudly(monkeypatch):
+    # No CPU or torch fallback exists: without libkvx every operator raises.
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", ROOT / "no-such-dir" / "libkvx.so")
+    with pytest.raises(RuntimeError, match="libkvx is not built"):
+        _lib.lib()
+    layout = ops.pool_layout(torch.zeros((2, 1, 2, 4, 1, 8), dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError, match="libkvx is not built"):
+        ops.entry_layout(layout, ops.FORMAT_FP8)
