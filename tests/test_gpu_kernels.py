@@ -342,3 +342,28 @@ def test_fp8_block_save_and_restore_replay_inside_a_hip_graph(gpu, scale_dtype):
             codes, scales = oracle.save_block_fp8(host_pool, b, scale_dtype == torch.float32)
             expect = oracle.dequantize(codes, scales, scale_dtype == torch.float32)
             assert np.array_equal(bf16_bits(replayed[:, :, d]), expect), (replay, b)
+
+
+def test_empty_and_all_padding_inputs_are_no_ops(gpu):
+    pool = make_pool(gpu, layers=2, blocks=3)
+    before = pool.clone()
+    heads, hd = pool.shape[4], pool.shape[5]
+    key = torch.randn((5, heads, hd), device=gpu).to(torch.bfloat16)
+    # No tokens; only padding slots (-1, decode graph padding); only slots outside the cache.
+    ops.store_kvcache(key[:0], key[:0], pool[0, 0], pool[1, 0], torch.empty(0, dtype=torch.int32, device=gpu))
+    ops.store_kvcache(key, key, pool[0, 0], pool[1, 0], torch.full((5,), -1, dtype=torch.int32, device=gpu))
+    outside = pool.shape[2] * pool.shape[3]
+    ops.store_kvcache(key, key, pool[0, 0], pool[1, 0],
+                      torch.arange(outside, outside + 5, dtype=torch.int32, device=gpu))
+    # Empty block lists and zero-row codec tensors.
+    ops.save_blocks(pool, [], [], ops.FORMAT_FP8, torch.float32)
+    ops.restore_blocks(pool, [], [], ops.FORMAT_RAW)
+    rows = pool[0, 0, 0, :0]
+    ops.fp8_quantize(rows, torch.empty(rows.shape, dtype=torch.float8_e4m3fn, device=gpu),
+                     torch.empty((*rows.shape[:-1], 1), dtype=torch.float32, device=gpu))
+    # Zero-token handoff copies.
+    dense = torch.empty((2, pool.shape[1], 0, heads, hd), dtype=pool.dtype, device=gpu)
+    ops.gather_tokens(pool, [], 0, dense)
+    ops.scatter_tokens(pool, [], 0, dense)
+    torch.cuda.synchronize()
+    assert torch.equal(pool.view(torch.int16), before.view(torch.int16))
