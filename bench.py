@@ -53,6 +53,7 @@ def parse_args():
     p.add_argument("--skip-store", action="store_true", help="skip the store_kvcache leg")
     p.add_argument("--skip-hybrid", action="store_true", help="skip the hybrid-admission calibration leg")
     p.add_argument("--skip-agents", action="store_true", help="skip the agent-pressure leg")
+    p.add_argument("--skip-handoff", action="store_true", help="skip the KV handoff leg")
     p.add_argument("--skip-reference-gpu", action="store_true",
                    help="skip timing the reference's torch codec chain on the GPU")
     p.add_argument("--skip-configs", action="store_true",
@@ -343,6 +344,66 @@ def reference_link_leg(torch, pool, sources, dests, scale_dtype, reps=3):
     both_s = timed(lambda: save(n), restore)
     return {"bytes_per_direction": link, "save_d2h_gbs": round(link / save_s / 1e9, 2),
             "restore_h2d_gbs": round(link / restore_s / 1e9, 2), "duplex_gbs": round(2 * link / both_s / 1e9, 2)}
+
+
+def handoff_leg(torch, pool, reps=3):
+    """KV handoff of one 32,767-token request (128 blocks) on the Qwen3-8B pool: export and import.
+
+    kvx: kv_handoff.export_kv / import_kv's copies (the token gather writes a
+    pinned host payload; the scatter reads it in place). Beside them, the
+    reference's copies for the same request on this GPU (kv_handoff.py:46-55:
+    index_select, pack, .cpu(); :112-118: .to(device), one copy_ per block).
+    """
+    from kvx import ops
+    from kvx.workloads import block_selection
+
+    _, layers, nb, bs, heads, hd = pool.shape
+    count = 128 * bs - 1
+    table = block_selection(nb, 128, seed=1)
+    dest = block_selection(nb, 128, seed=2)
+    shape = (2, layers, count, heads, hd)
+    nbytes = 2 * layers * count * heads * hd * pool.element_size()
+    stream = torch.cuda.current_stream(pool.device)
+
+    def timed(fn):
+        best = None
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            dt = time.perf_counter() - t0
+            best = dt if best is None else min(best, dt)
+        return best
+
+    snapshot = torch.empty(shape, dtype=pool.dtype, pin_memory=True)
+
+    def kvx_export():
+        ops.gather_tokens(pool, table, count, snapshot)
+        stream.synchronize()
+
+    def kvx_import():
+        ops.scatter_tokens(pool, dest, count, snapshot)
+
+    ids = torch.tensor(table, dtype=torch.int64, device=pool.device)
+    held = {}
+
+    def reference_export():
+        held["kv"] = pool.index_select(2, ids).flatten(2, 3)[:, :, :count].contiguous().cpu()
+
+    def reference_import():
+        payload = held["kv"].to(device=pool.device)
+        for logical, physical in enumerate(dest):
+            start = logical * bs
+            end = min(start + bs, count)
+            pool[:, :, physical, :end - start].copy_(payload[:, :, start:end])
+
+    out = {"tokens": count, "bytes": nbytes}
+    for name, fn in (("kvx_export", kvx_export), ("kvx_import", kvx_import),
+                     ("reference_export", reference_export), ("reference_import", reference_import)):
+        seconds = timed(fn)
+        out[name] = {"ms": round(1000 * seconds, 2), "gbs": round(nbytes / seconds / 1e9, 2)}
+    return out
 
 
 def bf16_leg(torch, ops, pool, reps, link=True):
@@ -679,6 +740,9 @@ def main():
         result["bf16_qwen3_8b"] = bf16_leg(torch, ops, pool, args.host_reps, link=not args.skip_host_link)
         log("qwen3-0.6b leg")
         result["fp8_qwen3_0_6b"] = qwen3_0_6b_leg(torch, ops, scale_dtype)
+    if not args.skip_handoff:
+        log("kv handoff leg")
+        result["kv_handoff"] = handoff_leg(torch, pool)
     if not args.skip_hybrid:
         log("hybrid calibration leg")
         result["hybrid_admission"] = hybrid_leg(torch, pool, scale_dtype)
