@@ -318,10 +318,10 @@ class BlockManager:
                         self._cpu_prefix_cache._copy_entry(entry, block_id)
                     self.blocks[block_id].update(h, token_ids)
                     self.hash_to_block_id[h] = block_id
-            for i in [*range(split), *range(num_cached_blocks, seq.num_blocks)]:
-                block_id = self._allocate_block()
-                owned.append(block_id)
-                table[i] = block_id
+                for i in [*range(split), *range(num_cached_blocks, seq.num_blocks)]:
+                    block_id = self._allocate_block()
+                    owned.append(block_id)
+                    table[i] = block_id
         except BaseException:
             for block_id in reversed(owned):
                 self._release_block(block_id)
@@ -358,8 +358,9 @@ class BlockManager:
         for i, block_id in enumerate(seq.block_table):
             self.blocks[block_id].release_gen = self._release_gen
             self.blocks[block_id].seq_index = i
-        for block_id in reversed(seq.block_table):
-            self._release_block(block_id)
+        with self._batched_copies():
+            for block_id in reversed(seq.block_table):
+                self._release_block(block_id)
         seq.num_cached_tokens = 0
         seq.restore_span = None
         seq.block_table.clear()

@@ -241,6 +241,9 @@ class CPUBlockCache:
         self._queued: list[tuple[int, int, bool]] = []  # (slot, block, wait) restores held back
         self._queued_blocks: set[int] = set()
         self._queued_slots: set[int] = set()
+        self._queued_saves: list[tuple[int, int]] = []  # (block, slot) saves held back
+        self._queued_save_slots: set[int] = set()
+        self._deferred_reuse: list[int] = []  # blocks whose before_block_reuse waits for held-back saves
         if automatic:
             if block_manager._cpu_prefix_cache is not None:
                 self._engine.close()
@@ -408,10 +411,16 @@ class CPUBlockCache:
             self._engine.synchronize()
 
     def _save_to_slot(self, block_id: int, slot: int):
-        """Queue pool block -> host slot on the save stream (the seam failure-injection tests patch)."""
+        """Queue pool block -> host slot on the save stream (held back inside coalesce())."""
         self._ensure_staging()
-        if block_id in self._queued_blocks or slot in self._queued_slots:
+        # A flush issues held-back saves before held-back restores, so a save that must follow one of them (it reads
+        # a block a restore writes, or writes a slot a restore reads or another save writes) flushes first.
+        if block_id in self._queued_blocks or slot in self._queued_slots or slot in self._queued_save_slots:
             self._flush()
+        if self._coalescing:
+            self._queued_saves.append((block_id, slot))
+            self._queued_save_slots.add(slot)
+            return
         self._engine.save([block_id], [slot], self._compute_stream())
 
     def _restore_from_slot(self, slot: int, block_id: int, wait: bool):
@@ -426,15 +435,19 @@ class CPUBlockCache:
 
     @contextmanager
     def coalesce(self):
-        """Hand the restores issued inside the block to the copy engine as batched calls on exit.
+        """Hand the saves and restores issued inside the block to the copy engine as batched calls on exit.
 
         One engine call per block costs a cross-stream wait per block: on
-        MI355X one-block restores ran at ~47 GB/s against ~55 GB/s for a batch.
-        Restores with wait=True make the caller's stream wait at the end of the
-        block instead of after each restore, so no work that reads a restored
-        block may be queued on that stream inside it. Anything that touches a
-        queued block or slot (a save, before_block_use/reuse, synchronize)
-        flushes the queue first. The block manager's admission and prefetch
+        MI355X one-block restores ran at ~47 GB/s against ~55 GB/s for a batch,
+        and one-block saves beside restores capped both directions together
+        near 60 GB/s. On exit the held-back saves go first (one call), then the
+        caller's stream waits for the blocks passed to before_block_reuse, then
+        the restores (one call per run of equal wait flags). Restores with
+        wait=True and before_block_reuse therefore make the caller's stream
+        wait at the end of the block, so no work that reads or writes those
+        blocks may be queued on that stream inside it. A save or restore that
+        must follow a held-back one, before_block_use of a held-back block and
+        synchronize flush first. The block manager's admission and prefetch
         loops use this.
         """
         self._coalescing += 1
@@ -446,8 +459,15 @@ class CPUBlockCache:
                 self._flush()
 
     def _flush(self):
+        saves, self._queued_saves, self._queued_save_slots = self._queued_saves, [], set()
+        reuse, self._deferred_reuse = self._deferred_reuse, []
         queued, self._queued = self._queued, []
         self._queued_blocks, self._queued_slots = set(), set()
+        compute = self._compute_stream()
+        if saves:
+            self._engine.save([block for block, _ in saves], [slot for _, slot in saves], compute)
+        for block_id in reuse:
+            self._engine.before_block_reuse(block_id, compute)
         start = 0
         while start < len(queued):
             end, wait = start, queued[start][2]
@@ -516,6 +536,9 @@ class CPUBlockCache:
         """Order later writes to a GPU block after its pending save and restore, without a host sync."""
         if block_id in self._queued_blocks:
             self._flush()
+        if self._queued_saves:
+            self._deferred_reuse.append(block_id)  # after the held-back saves, at the end of coalesce()
+            return
         self._engine.before_block_reuse(block_id, self._compute_stream())
 
     def before_block_use(self, block_id: int):

@@ -370,3 +370,31 @@ def test_coalesced_restores_land_before_dependent_work(gpu):
     assert np.array_equal(u8(copy5), expected[keys[2]])
     assert np.array_equal(u8(cache._entries[keys[1]].kv), expected[keys[1]])
     cache.close()
+
+
+def test_coalesced_saves_and_reuse_waits_keep_victims_intact(gpu):
+    pool = make_pool(gpu, 4)
+    manager = BlockManager(4, BS)
+    keys = [publish(manager, b, 40 + b) for b in range(2)]
+    expected = {k: block_bytes(pool, b) for b, k in enumerate(keys)}
+    cache = new_cache(pool, manager, blocks=3, split_streams=True)
+    slow_copies(cache)
+    with cache.coalesce():
+        for b, k in enumerate(keys):
+            assert cache.save_block(k)
+            cache.before_block_reuse(b)  # recycling the victim: deferred behind the held-back save
+        assert len(cache._queued_saves) == 2 and cache._deferred_reuse == [0, 1]
+        # A second save into a slot a held-back save writes flushes first.
+        slot = cache._entries[keys[1]].slot
+        cache.discard(keys[1])
+        assert cache._free_slots[-1] == slot
+        keys.append(publish(manager, 2, 42))
+        expected[keys[2]] = block_bytes(pool, 2)
+        assert cache.save_block(keys[2]) and not cache._deferred_reuse
+        cache.before_block_reuse(2)
+        assert cache._deferred_reuse == [2]
+    pool[:, :, 0:3].fill_(-1)  # compute overwrites the victims after the block
+    cache.synchronize()
+    for k in (keys[0], keys[2]):
+        assert np.array_equal(u8(cache._entries[k].kv), expected[k]), k
+    cache.close()
