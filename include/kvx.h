@@ -176,9 +176,12 @@ int kvx_cache_streams(kvx_cache* cache, void** save_stream, void** restore_strea
 /*
  * Saves pool blocks block_ids_host[i] into host slots slots_host[i]
  * (save_block, :306-322). The save stream first waits for all work queued
- * on compute_stream and for the last restore that read each slot; a "save
- * done" event then marks each block (for before_block_reuse) and each slot
- * (for a later restore of it).
+ * on compute_stream, for the last restore that read each slot and for any
+ * background restore still writing each block; a "save done" event then
+ * marks each block (for before_block_reuse) and each slot (for a later
+ * restore of it). Calls of at most 256 MiB of entries have the save kernel
+ * write the slots itself; larger ones go through device staging and DMA.
+ * Slabs must be pinned, device-accessible host memory (hipHostMalloc).
  */
 int kvx_cache_save(kvx_cache* cache, const int32_t* block_ids_host, const int32_t* slots_host,
                    int32_t n, void* compute_stream);
