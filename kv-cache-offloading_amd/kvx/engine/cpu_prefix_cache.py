@@ -163,6 +163,95 @@ class _CopyEngine:
             check(lib().kvx_cache_destroy(handle), "kvx_cache_destroy")
 
 
+class _CopyBatcher:
+    """Hands a cache's saves and restores to its copy engine, in batches inside coalesce().
+
+    One engine call per block costs a cross-stream wait per block: on MI355X
+    one-block restores ran at ~47 GB/s against ~55 GB/s for a batch, and
+    one-block saves beside restores capped both directions together near
+    60 GB/s. Inside coalesce() saves, restores and before_block_reuse waits
+    are held back; on exit the saves go first (one call), then the caller's
+    stream waits for the blocks passed to before_block_reuse, then the
+    restores (one call per run of equal wait flags). Restores with wait=True
+    and before_block_reuse therefore take effect at the end of the block, so
+    no work that reads or writes those blocks may be queued on the caller's
+    stream inside it. Anything that must follow a held-back copy flushes
+    first: a save of a block a held-back restore writes, a save into a slot a
+    held-back restore reads or a held-back save writes, before_block_use or
+    before_block_reuse of a block with a held-back restore.
+    """
+
+    def __init__(self, engine, compute_stream):
+        self.engine = engine
+        self._compute = compute_stream  # () -> the caller's current stream handle
+        self.depth = 0
+        self.saves: list[tuple[int, int]] = []  # (block, slot)
+        self.save_slots: set[int] = set()
+        self.reuse: list[int] = []  # blocks whose before_block_reuse waits come after the saves
+        self.restores: list[tuple[int, int, bool]] = []  # (slot, block, wait)
+        self.restore_blocks: set[int] = set()
+        self.restore_slots: set[int] = set()
+
+    def save(self, block_id: int, slot: int):
+        if block_id in self.restore_blocks or slot in self.restore_slots or slot in self.save_slots:
+            self.flush()
+        if self.depth:
+            self.saves.append((block_id, slot))
+            self.save_slots.add(slot)
+            return
+        self.engine.save([block_id], [slot], self._compute())
+
+    def restore(self, slot: int, block_id: int, wait: bool):
+        if self.depth:
+            self.restores.append((slot, block_id, wait))
+            self.restore_blocks.add(block_id)
+            self.restore_slots.add(slot)
+            return
+        self.engine.restore([slot], [block_id], wait, self._compute())
+
+    def before_block_reuse(self, block_id: int):
+        if block_id in self.restore_blocks:
+            self.flush()
+        if self.saves:
+            self.reuse.append(block_id)
+            return
+        self.engine.before_block_reuse(block_id, self._compute())
+
+    def before_block_use(self, block_id: int):
+        if block_id in self.restore_blocks:
+            self.flush()
+        self.engine.before_block_use(block_id, self._compute())
+
+    @contextmanager
+    def coalesce(self):
+        self.depth += 1
+        try:
+            yield
+        finally:
+            self.depth -= 1
+            if not self.depth:
+                self.flush()
+
+    def flush(self):
+        saves, self.saves, self.save_slots = self.saves, [], set()
+        reuse, self.reuse = self.reuse, []
+        restores, self.restores = self.restores, []
+        self.restore_blocks, self.restore_slots = set(), set()
+        compute = self._compute()
+        if saves:
+            self.engine.save([block for block, _ in saves], [slot for _, slot in saves], compute)
+        for block_id in reuse:
+            self.engine.before_block_reuse(block_id, compute)
+        start = 0
+        while start < len(restores):
+            end, wait = start, restores[start][2]
+            while end < len(restores) and restores[end][2] == wait:
+                end += 1
+            run = restores[start:end]
+            self.engine.restore([slot for slot, _, _ in run], [block for _, block, _ in run], wait, compute)
+            start = end
+
+
 class CPUBlockCache:
     """One engine's bounded payload store, with optional automatic integration.
 
@@ -237,13 +326,7 @@ class CPUBlockCache:
         self._copy_stream = self._engine.save_stream
         self._restore_stream = self._engine.restore_stream
         self._staging: list[torch.Tensor] = []
-        self._coalescing = 0  # depth of coalesce() blocks
-        self._queued: list[tuple[int, int, bool]] = []  # (slot, block, wait) restores held back
-        self._queued_blocks: set[int] = set()
-        self._queued_slots: set[int] = set()
-        self._queued_saves: list[tuple[int, int]] = []  # (block, slot) saves held back
-        self._queued_save_slots: set[int] = set()
-        self._deferred_reuse: list[int] = []  # blocks whose before_block_reuse waits for held-back saves
+        self._batcher = _CopyBatcher(self._engine, self._compute_stream)
         if automatic:
             if block_manager._cpu_prefix_cache is not None:
                 self._engine.close()
@@ -407,76 +490,23 @@ class CPUBlockCache:
     def synchronize(self):
         """Wait for every pending host<->device copy (needed before host reads)."""
         if not self.closed:
-            self._flush()
+            self._batcher.flush()
             self._engine.synchronize()
 
     def _save_to_slot(self, block_id: int, slot: int):
-        """Queue pool block -> host slot on the save stream (held back inside coalesce())."""
+        """Queue pool block -> host slot on the save stream (the seam failure-injection tests patch)."""
         self._ensure_staging()
-        # A flush issues held-back saves before held-back restores, so a save that must follow one of them (it reads
-        # a block a restore writes, or writes a slot a restore reads or another save writes) flushes first.
-        if block_id in self._queued_blocks or slot in self._queued_slots or slot in self._queued_save_slots:
-            self._flush()
-        if self._coalescing:
-            self._queued_saves.append((block_id, slot))
-            self._queued_save_slots.add(slot)
-            return
-        self._engine.save([block_id], [slot], self._compute_stream())
+        self._batcher.save(block_id, slot)
 
     def _restore_from_slot(self, slot: int, block_id: int, wait: bool):
-        """Queue host slot -> pool block on the restore stream (held back inside coalesce())."""
+        """Queue host slot -> pool block on the restore stream."""
         self._ensure_staging()
-        if self._coalescing:
-            self._queued.append((slot, block_id, wait))
-            self._queued_blocks.add(block_id)
-            self._queued_slots.add(slot)
-            return
-        self._engine.restore([slot], [block_id], wait, self._compute_stream())
+        self._batcher.restore(slot, block_id, wait)
 
-    @contextmanager
     def coalesce(self):
-        """Hand the saves and restores issued inside the block to the copy engine as batched calls on exit.
-
-        One engine call per block costs a cross-stream wait per block: on
-        MI355X one-block restores ran at ~47 GB/s against ~55 GB/s for a batch,
-        and one-block saves beside restores capped both directions together
-        near 60 GB/s. On exit the held-back saves go first (one call), then the
-        caller's stream waits for the blocks passed to before_block_reuse, then
-        the restores (one call per run of equal wait flags). Restores with
-        wait=True and before_block_reuse therefore make the caller's stream
-        wait at the end of the block, so no work that reads or writes those
-        blocks may be queued on that stream inside it. A save or restore that
-        must follow a held-back one, before_block_use of a held-back block and
-        synchronize flush first. The block manager's admission and prefetch
-        loops use this.
-        """
-        self._coalescing += 1
-        try:
-            yield
-        finally:
-            self._coalescing -= 1
-            if not self._coalescing:
-                self._flush()
-
-    def _flush(self):
-        saves, self._queued_saves, self._queued_save_slots = self._queued_saves, [], set()
-        reuse, self._deferred_reuse = self._deferred_reuse, []
-        queued, self._queued = self._queued, []
-        self._queued_blocks, self._queued_slots = set(), set()
-        compute = self._compute_stream()
-        if saves:
-            self._engine.save([block for block, _ in saves], [slot for _, slot in saves], compute)
-        for block_id in reuse:
-            self._engine.before_block_reuse(block_id, compute)
-        start = 0
-        while start < len(queued):
-            end, wait = start, queued[start][2]
-            while end < len(queued) and queued[end][2] == wait:
-                end += 1
-            run = queued[start:end]
-            self._engine.restore([slot for slot, _, _ in run], [block for _, block, _ in run], wait,
-                                 self._compute_stream())
-            start = end
+        """Batch the saves and restores issued inside a `with` block (see _CopyBatcher); used by the block
+        manager's admission, prefetch and release loops."""
+        return self._batcher.coalesce()
 
     def save_block(self, prefix_hash: int) -> bool:
         """Save a published full block; return False if already saved (cpu_prefix_cache.py:275-332).
@@ -534,18 +564,11 @@ class CPUBlockCache:
 
     def before_block_reuse(self, block_id: int):
         """Order later writes to a GPU block after its pending save and restore, without a host sync."""
-        if block_id in self._queued_blocks:
-            self._flush()
-        if self._queued_saves:
-            self._deferred_reuse.append(block_id)  # after the held-back saves, at the end of coalesce()
-            return
-        self._engine.before_block_reuse(block_id, self._compute_stream())
+        self._batcher.before_block_reuse(block_id)
 
     def before_block_use(self, block_id: int):
         """Order later reads of a prefetched GPU block after its restore."""
-        if block_id in self._queued_blocks:
-            self._flush()
-        self._engine.before_block_use(block_id, self._compute_stream())
+        self._batcher.before_block_use(block_id)
 
     def _entry_for(self, prefix_hash: int, token_ids):
         """Pure lookup used while planning admission."""

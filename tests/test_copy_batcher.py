@@ -1,0 +1,135 @@
+"""The cache's batching rules, driven with a recording copy engine (CPU only).
+
+The GPU tests show that batched copies land in order on the device; these pin
+which engine calls the batcher makes and when: outside coalesce() every call
+goes straight through, inside it saves, before_block_reuse waits and restores
+are held back and flushed as saves -> reuse waits -> restores (one call per
+run of equal wait flags), and a copy that must follow a held-back one flushes
+first. A batcher that reordered the flush (restores before saves, or reuse
+waits before the saves they wait on) fails here.
+"""
+
+import pytest
+
+from kvx.engine.cpu_prefix_cache import _CopyBatcher
+
+STREAM = 7
+
+
+class RecordingEngine:
+    def __init__(self):
+        self.calls = []
+
+    def save(self, blocks, slots, stream):
+        assert stream == STREAM
+        self.calls.append(("save", list(blocks), list(slots)))
+
+    def restore(self, slots, blocks, wait, stream):
+        assert stream == STREAM
+        self.calls.append(("restore", list(slots), list(blocks), wait))
+
+    def before_block_reuse(self, block, stream):
+        assert stream == STREAM
+        self.calls.append(("reuse", block))
+
+    def before_block_use(self, block, stream):
+        assert stream == STREAM
+        self.calls.append(("use", block))
+
+
+def make():
+    engine = RecordingEngine()
+    return engine, _CopyBatcher(engine, lambda: STREAM)
+
+
+def test_calls_go_straight_through_outside_coalesce():
+    engine, batcher = make()
+    batcher.save(3, 0)
+    batcher.before_block_reuse(3)
+    batcher.restore(0, 5, True)
+    batcher.before_block_use(5)
+    assert engine.calls == [("save", [3], [0]), ("reuse", 3), ("restore", [0], [5], True), ("use", 5)]
+
+
+def test_flush_order_is_saves_then_reuse_waits_then_restore_runs():
+    engine, batcher = make()
+    with batcher.coalesce():
+        batcher.restore(10, 1, True)
+        batcher.save(2, 20)
+        batcher.before_block_reuse(2)
+        batcher.restore(11, 3, True)
+        batcher.restore(12, 4, False)
+        batcher.save(5, 21)
+        batcher.before_block_reuse(5)
+        batcher.restore(13, 6, True)
+        assert engine.calls == []
+    assert engine.calls == [
+        ("save", [2, 5], [20, 21]),
+        ("reuse", 2),
+        ("reuse", 5),
+        ("restore", [10, 11], [1, 3], True),
+        ("restore", [12], [4], False),
+        ("restore", [13], [6], True),
+    ]
+    assert not (batcher.saves or batcher.reuse or batcher.restores)
+
+
+def test_reuse_wait_without_held_back_saves_is_immediate():
+    engine, batcher = make()
+    with batcher.coalesce():
+        batcher.restore(10, 1, False)
+        batcher.before_block_reuse(2)  # nothing held back that block 2's save could be
+        assert engine.calls == [("reuse", 2)]
+    assert engine.calls[-1] == ("restore", [10], [1], False)
+
+
+@pytest.mark.parametrize("conflict, call, after", [
+    ("save of a block a held-back restore writes", lambda b: b.save(2, 21), ("save", [2], [21])),
+    ("save into a slot a held-back restore reads", lambda b: b.save(3, 10), ("save", [3], [10])),
+    ("save into a slot a held-back save writes", lambda b: b.save(3, 20), ("save", [3], [20])),
+    ("use of a block a held-back restore writes", lambda b: b.before_block_use(2), ("use", 2)),
+    ("reuse of a block a held-back restore writes", lambda b: b.before_block_reuse(2), ("reuse", 2)),
+])
+def test_conflicts_flush_first(conflict, call, after):
+    engine, batcher = make()
+    flushed = [("save", [1], [20]), ("restore", [10], [2], True)]
+    with batcher.coalesce():
+        batcher.save(1, 20)
+        batcher.restore(10, 2, True)
+        call(batcher)
+        # The conflicting call comes after the flush; a save is held back again until the block ends.
+        assert engine.calls == flushed + ([] if after[0] == "save" else [after]), conflict
+    assert engine.calls == flushed + [after], conflict
+
+
+def test_use_of_an_unqueued_block_does_not_flush():
+    engine, batcher = make()
+    with batcher.coalesce():
+        batcher.restore(10, 2, True)
+        batcher.before_block_use(7)
+        assert engine.calls == [("use", 7)]
+    assert engine.calls[-1] == ("restore", [10], [2], True)
+
+
+def test_nested_blocks_flush_once_at_the_outer_end():
+    engine, batcher = make()
+    with batcher.coalesce():
+        batcher.save(1, 20)
+        with batcher.coalesce():
+            batcher.restore(10, 2, False)
+        assert engine.calls == []
+        batcher.restore(11, 3, False)
+    assert engine.calls == [("save", [1], [20]), ("restore", [10, 11], [2, 3], False)]
+
+
+def test_exception_inside_the_block_still_issues_queued_copies():
+    engine, batcher = make()
+    with pytest.raises(KeyError):
+        with batcher.coalesce():
+            batcher.save(1, 20)
+            batcher.restore(10, 2, True)
+            raise KeyError("admission failed")
+    assert engine.calls == [("save", [1], [20]), ("restore", [10], [2], True)]
+    assert batcher.depth == 0
+    batcher.save(4, 21)  # back to immediate calls
+    assert engine.calls[-1] == ("save", [4], [21])

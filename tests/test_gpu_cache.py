@@ -354,14 +354,14 @@ def test_coalesced_restores_land_before_dependent_work(gpu):
     with cache.coalesce():
         cache._copy_entry(entries[0], 3)  # wait=True: compute waits when the block ends
         cache._copy_entry(entries[1], 4, wait=False)
-        assert len(cache._queued) == 2  # held back
+        assert len(cache._batcher.restores) == 2  # held back
         # A save of a queued block flushes first and reads the restored bytes.
         manager.blocks[4].update(keys[1], [21] * BS)
         manager.hash_to_block_id[keys[1]] = 4
         cache.discard(keys[1])
-        assert cache.save_block(keys[1]) and not cache._queued
+        assert cache.save_block(keys[1]) and not cache._batcher.restores
         cache._copy_entry(entries[2], 5, wait=False)
-    assert not cache._queued
+    assert not cache._batcher.restores
     copy = pool[:, :, 3].clone()  # compute-stream work after the block sees the restored bytes
     cache.before_block_use(5)
     copy5 = pool[:, :, 5].clone()
@@ -383,16 +383,16 @@ def test_coalesced_saves_and_reuse_waits_keep_victims_intact(gpu):
         for b, k in enumerate(keys):
             assert cache.save_block(k)
             cache.before_block_reuse(b)  # recycling the victim: deferred behind the held-back save
-        assert len(cache._queued_saves) == 2 and cache._deferred_reuse == [0, 1]
+        assert len(cache._batcher.saves) == 2 and cache._batcher.reuse == [0, 1]
         # A second save into a slot a held-back save writes flushes first.
         slot = cache._entries[keys[1]].slot
         cache.discard(keys[1])
         assert cache._free_slots[-1] == slot
         keys.append(publish(manager, 2, 42))
         expected[keys[2]] = block_bytes(pool, 2)
-        assert cache.save_block(keys[2]) and not cache._deferred_reuse
+        assert cache.save_block(keys[2]) and not cache._batcher.reuse
         cache.before_block_reuse(2)
-        assert cache._deferred_reuse == [2]
+        assert cache._batcher.reuse == [2]
     pool[:, :, 0:3].fill_(-1)  # compute overwrites the victims after the block
     cache.synchronize()
     for k in (keys[0], keys[2]):
