@@ -207,7 +207,9 @@ def agent_leg(torch, pool, scale_dtype):
     prefetch restores of each returning agent's prefix, KV written by
     store_kvcache. Run once with split save/restore streams and once with one
     copy stream; link GB/s is entry bytes moved over the run's wall time
-    (engine, scheduling and the synthetic model included).
+    (engine, scheduling and the synthetic model included). Each cache pins its
+    whole budget when it is created (the reference's preallocate option), so
+    neither run's time includes page-locking host memory.
     """
     from kvx.engine.llm_engine import LLMEngine
     from kvx.workloads import SyntheticKVRunner, run_agent_pressure
@@ -217,7 +219,7 @@ def agent_leg(torch, pool, scale_dtype):
         engine = LLMEngine(SyntheticKVRunner(pool), max_num_batched_tokens=16384, max_num_seqs=4, eos=-1,
                            kvcache_block_size=pool.shape[3], num_kvcache_blocks=pool.shape[2])
         engine.create_cpu_prefix_cache(8 << 30, automatic=True, prefetch=True, split_streams=split, fp8=True,
-                                       scale_dtype=scale_dtype)
+                                       scale_dtype=scale_dtype, preallocate=True)
         try:
             r = run_agent_pressure(engine, agents=4, context=32768, turns=12, append=2048, verify=False)
         finally:

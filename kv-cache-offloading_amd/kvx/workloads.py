@@ -201,9 +201,12 @@ def run_agent_pressure(engine, agents: int = 4, context: int = 32768, turns: int
 
     With verify=True every `verify_stride`-th full block (and the last) of each finished request must hold
     either the exact synthetic KV (GPU hit or recomputed) or its FP8 round trip (restored from an FP8 entry) --
-    a block restored from the wrong slot, or read before its restore finished, matches neither. Before each
-    request the next agent's prefix is hinted with prefetch_prefix, so its restores (H2D) overlap the saves
-    (D2H) of the blocks the current request evicts.
+    a block restored from the wrong slot, or read before its restore finished, matches neither. After each
+    request's first step (or, if that step finished it, after it is checked) the next agent's prefix is hinted
+    with prefetch_prefix, so its restores (H2D) overlap the rest of the current request and the saves (D2H) of
+    the blocks it evicts. Hinting before the current request's admission instead would let the prefetch evict
+    the current agent's own cached blocks (the least recently used ones), which its admission would then
+    restore again.
     """
     import time
 
@@ -221,13 +224,14 @@ def run_agent_pressure(engine, agents: int = 4, context: int = 32768, turns: int
     for turn in range(turns):
         for a in range(agents):
             histories[a] += torch.randint(2, 50000, (append,), generator=g).tolist()
-            if prefetch_hints and agents > 1:
-                nxt = (a + 1) % agents
-                engine.prefetch_prefix(Sequence(histories[nxt]))
-            seq_id = engine.add_request(histories[a], params)
-            seq = next(s for s in engine.scheduler.waiting if s.seq_id == seq_id)
+            engine.add_request(histories[a], params)
+            nxt = Sequence(histories[(a + 1) % agents]) if prefetch_hints and agents > 1 else None
             while not engine.is_finished():
                 engine.step()
+                if nxt is not None and not engine.is_finished():
+                    # After this request's admission, so the prefetch takes other agents' blocks, not its own.
+                    engine.prefetch_prefix(nxt)
+                    nxt = None
             histories[a] += [engine.model_runner.next_token]
             if verify:
                 # The request's full blocks are now idle GPU hits: check a sample of them.
@@ -259,6 +263,9 @@ def run_agent_pressure(engine, agents: int = 4, context: int = 32768, turns: int
                                              "neither its KV nor the FP8 round trip of it")
                     checked += 1
                     fp8_hits += 1
+            if nxt is not None:
+                # The request finished in one step: hint once it is checked (the prefetch may recycle its blocks).
+                engine.prefetch_prefix(nxt)
     if cache is not None:
         cache.synchronize()
     torch.cuda.synchronize(pool.device)
