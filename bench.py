@@ -117,8 +117,11 @@ def store_leg(torch, ops, pool, reps=5):
     """store_kvcache over all layers for a ragged batch of 16 sequences (lengths U[1, 8192], seeded).
 
     K is contiguous; V is a strided view of a fused QKV output (row stride
-    (32 + 2H) * hd, as Qwen3-8B's). Slots are distinct random pool slots;
-    the batch is padded to a multiple of 256 with -1 slots.
+    (32 + 2H) * hd, as Qwen3-8B's). The headline slots are distinct random
+    pool slots, token by token (the worst case for the writes); the batch is
+    padded to a multiple of 256 with -1 slots. `paged_blocks` times the same
+    batch with the slot layout a model runner produces (model_runner.py:156-166):
+    each sequence gets seeded random distinct blocks and fills them in order.
     """
     import numpy as np
 
@@ -133,30 +136,54 @@ def store_leg(torch, ops, pool, reps=5):
     qkv = torch.randn((padded, (32 + 2 * heads) * hd), generator=g, device=pool.device).to(torch.bfloat16)
     key = qkv[:, 32 * hd:(32 + heads) * hd].contiguous().view(padded, heads, hd)
     value = qkv[:, (32 + heads) * hd:].view(padded, heads, hd)
-    mapping = torch.from_numpy(slots).to(pool.device)
     stream = torch.cuda.current_stream(pool.device)
-
-    def run():
-        for layer in range(layers):
-            ops.store_kvcache(key, value, pool[0, layer], pool[1, layer], mapping)
-
-    run()
-    times = []
-    for _ in range(reps):
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        run()
-        end.record(stream)
-        end.synchronize()
-        times.append(start.elapsed_time(end) / 1000)
-    t = sorted(times)[len(times) // 2]
     row = heads * hd * 2
-    per_launch = total * 4 * row + padded * 4  # K and V rows read and written, plus the slot map
-    gbs = layers * per_launch / t / 1e9
+
+    def timed(slot_map, tokens):
+        mapping = torch.from_numpy(slot_map).to(pool.device)
+
+        def run():
+            for layer in range(layers):
+                ops.store_kvcache(key, value, pool[0, layer], pool[1, layer], mapping)
+
+        run()
+        times = []
+        for _ in range(reps):
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            run()
+            end.record(stream)
+            end.synchronize()
+            times.append(start.elapsed_time(end) / 1000)
+        t = sorted(times)[len(times) // 2]
+        per_launch = tokens * 4 * row + padded * 4  # K and V rows read and written, plus the slot map
+        gbs = layers * per_launch / t / 1e9
+        return t, per_launch, gbs
+
+    t, per_launch, gbs = timed(slots, total)
     traffic, _ = pmc_traffic("store_kv_vec<")
-    return {"tokens": total, "padded_tokens": padded, "layers": layers, "ms_all_layers": round(1000 * t, 4),
-            "algorithmic_bytes_per_launch": per_launch, "hbm_gbs": round(gbs, 1),
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic}
+    out = {"tokens": total, "padded_tokens": padded, "layers": layers, "ms_all_layers": round(1000 * t, 4),
+           "algorithmic_bytes_per_launch": per_launch, "hbm_gbs": round(gbs, 1),
+           "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic}
+
+    paged = np.full(padded, -1, dtype=np.int32)
+    blocks = iter(rng.permutation(nb).tolist())
+    pos = 0
+    for length in lengths.tolist():
+        need = -(-length // bs)
+        if pos + length > padded or need > nb:
+            break
+        table = [next(blocks, None) for _ in range(need)]
+        if None in table:
+            break
+        seq_slots = (np.asarray(table, dtype=np.int64)[:, None] * bs + np.arange(bs)).reshape(-1)[:length]
+        paged[pos:pos + length] = seq_slots
+        pos += length
+    t, per_launch, gbs = timed(paged, pos)
+    out["paged_blocks"] = {"tokens": pos, "ms_all_layers": round(1000 * t, 4),
+                           "algorithmic_bytes_per_launch": per_launch, "hbm_gbs": round(gbs, 1),
+                           "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    return out
 
 
 # Recompute cost coefficients the reference's replay harness defaults to
