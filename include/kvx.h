@@ -109,7 +109,8 @@ int kvx_store_kvcache(const void* key, int64_t key_stride, const void* value, in
  * device-accessible byte address of entry i (device staging or mapped
  * pinned host memory). For FP8 the scales of entry i are at
  * entries_host[i] + scale_offset (may be negative). n may exceed the
- * per-launch batch; the call splits it.
+ * per-launch batch; the call splits it. No two payload or scale ranges may
+ * overlap (KVX_E_INVALID).
  */
 int kvx_save_blocks(const void* pool, const kvx_block_layout* layout, int32_t format,
                     const int32_t* block_ids_host, const uint64_t* entries_host, int32_t n,
@@ -119,7 +120,8 @@ int kvx_save_blocks(const void* pool, const kvx_block_layout* layout, int32_t fo
  * Restore n entries into pool blocks. Replaces _copy_entry's copy
  * (nanovllm/engine/cpu_prefix_cache.py:383-386): FP8 format runs
  * fp8_dequantize (:27-28) via _dequantize (:236-243) into pool[:, :, block];
- * RAW format is target.copy_(entry.kv) (:386). Arguments as kvx_save_blocks.
+ * RAW format is target.copy_(entry.kv) (:386). Arguments as kvx_save_blocks;
+ * a block may appear only once per call (KVX_E_INVALID).
  */
 int kvx_restore_blocks(void* pool, const kvx_block_layout* layout, int32_t format,
                        const int32_t* block_ids_host, const uint64_t* entries_host, int32_t n,
@@ -134,6 +136,7 @@ int kvx_restore_blocks(void* pool, const kvx_block_layout* layout, int32_t forma
  * kvx_gather_tokens replaces export_kv's index_select + contiguous
  * (:46-55); kvx_scatter_tokens replaces import_kv's per-block copy_
  * (:112-118). The buffer may be device memory or mapped pinned host memory.
+ * A scatter's table may not name a block twice (KVX_E_INVALID).
  */
 int kvx_gather_tokens(const void* pool, const kvx_block_layout* layout, const int32_t* block_table_host,
                       int32_t table_len, int64_t num_rows, void* dst, void* stream);
@@ -182,6 +185,7 @@ int kvx_cache_streams(kvx_cache* cache, void** save_stream, void** restore_strea
  * restore of it). Calls of at most 256 MiB of entries have the save kernel
  * write the slots itself; larger ones go through device staging and DMA.
  * Slabs must be pinned, device-accessible host memory (hipHostMalloc).
+ * A slot may appear only once per call (KVX_E_INVALID).
  */
 int kvx_cache_save(kvx_cache* cache, const int32_t* block_ids_host, const int32_t* slots_host,
                    int32_t n, void* compute_stream);
@@ -191,7 +195,8 @@ int kvx_cache_save(kvx_cache* cache, const int32_t* block_ids_host, const int32_
  * each slot's save, and for any pending save of each destination block (the
  * write-after-read order the reference leaves to its callers). With
  * wait != 0 compute_stream waits for the restore; otherwise the block is
- * marked pending until before_block_use/before_block_reuse.
+ * marked pending until before_block_use/before_block_reuse. A block may
+ * appear only once per call (KVX_E_INVALID).
  */
 int kvx_cache_restore(kvx_cache* cache, const int32_t* slots_host, const int32_t* block_ids_host,
                       int32_t n, int32_t wait, void* compute_stream);

@@ -6,6 +6,7 @@
 
 #include <algorithm>
 #include <new>
+#include <utility>
 #include <vector>
 
 #include "kvx_internal.h"
@@ -73,6 +74,23 @@ static void entry_sizes(const kvx_block_layout& l, int32_t format, int64_t* logi
   *stride = (bytes + 255) / 256 * 256;
 }
 
+// True if two of the n values are equal: two copies into one destination
+// in one call would race, so calls reject it.
+static bool any_repeat(const int32_t* v, int64_t n) {
+  if (n < 2) return false;
+  std::vector<int32_t> s(v, v + n);
+  std::sort(s.begin(), s.end());
+  return std::adjacent_find(s.begin(), s.end()) != s.end();
+}
+
+// True if two of the byte ranges [start, end) share a byte.
+static bool any_overlap(std::vector<std::pair<uint64_t, uint64_t>>& ranges) {
+  std::sort(ranges.begin(), ranges.end());
+  for (size_t i = 1; i < ranges.size(); ++i)
+    if (ranges[i].first < ranges[i - 1].second) return true;
+  return false;
+}
+
 // Splits (ids, entries) into launches of at most kMaxBatch blocks.
 static int run_batches(bool save, void* pool, const kvx_block_layout* layout, int32_t format,
                        const int32_t* ids, const uint64_t* entries, int32_t n, int64_t scale_offset,
@@ -95,6 +113,24 @@ static int run_batches(bool save, void* pool, const kvx_block_layout* layout, in
       return set_error(KVX_E_INVALID, "scales of entry %d are misaligned", i);
   }
   if ((uintptr_t)pool % 2) return set_error(KVX_E_INVALID, "pool is not 2-byte aligned");
+  if (save) {
+    // Entries are written: no payload or scale range may share a byte with another.
+    const int64_t rows = (int64_t)layout->planes * layout->plane_rows;
+    const bool fp8 = format == KVX_FORMAT_FP8;
+    const uint64_t payload = (uint64_t)(rows * layout->head_dim * (fp8 ? 1 : layout->elem_bytes));
+    std::vector<std::pair<uint64_t, uint64_t>> ranges;
+    ranges.reserve(fp8 ? 2 * (size_t)n : (size_t)n);
+    for (int32_t i = 0; i < n; ++i) {
+      ranges.emplace_back(entries[i], entries[i] + payload);
+      if (fp8) {
+        const uint64_t scales = entries[i] + (uint64_t)scale_offset;
+        ranges.emplace_back(scales, scales + (uint64_t)(rows * sbytes));
+      }
+    }
+    if (any_overlap(ranges)) return set_error(KVX_E_INVALID, "entries or their scales overlap in one save");
+  } else if (any_repeat(ids, n)) {
+    return set_error(KVX_E_INVALID, "a block appears twice in one restore");
+  }
   BlockBatch b;
   for (int32_t base = 0; base < n; base += kMaxBatch) {
     b.n = std::min(kMaxBatch, n - base);
@@ -128,6 +164,7 @@ static int token_copy(bool gather, void* pool, const kvx_block_layout* l, const 
   for (int64_t i = 0; i < nblocks; ++i)
     if (table[i] < 0 || table[i] >= l->num_blocks)
       return set_error(KVX_E_RANGE, "block id %d outside [0, %d)", table[i], l->num_blocks);
+  if (!gather && any_repeat(table, nblocks)) return set_error(KVX_E_INVALID, "a block appears twice in one scatter");
   const int64_t dense_plane_stride = num_rows * row_bytes;
   const int64_t tail_bytes = (num_rows - (nblocks - 1) * l->plane_rows) * row_bytes;
   BlockBatch b;
@@ -264,7 +301,8 @@ struct kvx_cache {
     return hip_status(hipStreamWaitEvent(dst, marker, 0), "hipStreamWaitEvent");
   }
 
-  int check_lists(const int32_t* ids, const int32_t* slots, int32_t n) const {
+  // `save`: the slots are destinations and must be distinct; otherwise the blocks are.
+  int check_lists(bool save, const int32_t* ids, const int32_t* slots, int32_t n) const {
     if (n < 0) return set_error(KVX_E_INVALID, "negative block count");
     if (n > 0 && (!ids || !slots)) return set_error(KVX_E_INVALID, "NULL block id or slot array");
     for (int32_t i = 0; i < n; ++i) {
@@ -273,6 +311,8 @@ struct kvx_cache {
       if (slots[i] < 0 || slots[i] >= num_slots)
         return set_error(KVX_E_RANGE, "host slot %d outside [0, %d)", slots[i], num_slots);
     }
+    if (any_repeat(save ? slots : ids, n))
+      return set_error(KVX_E_INVALID, save ? "a slot appears twice in one save" : "a block appears twice in one restore");
     if (n > 0 && !save_staging) return set_error(KVX_E_STATE, "no staging attached");
     return KVX_OK;
   }
@@ -513,7 +553,7 @@ int kvx_cache_streams(kvx_cache* c, void** save_stream, void** restore_stream) {
 
 int kvx_cache_save(kvx_cache* c, const int32_t* ids, const int32_t* slots, int32_t n, void* compute_stream) {
   if (!c) return set_error(KVX_E_INVALID, "NULL cache");
-  int rc = c->check_lists(ids, slots, n);
+  int rc = c->check_lists(true, ids, slots, n);
   if (rc || n == 0) return rc;
   DeviceScope scope;
   rc = scope.enter(c->device);
@@ -575,7 +615,7 @@ int kvx_cache_save(kvx_cache* c, const int32_t* ids, const int32_t* slots, int32
 int kvx_cache_restore(kvx_cache* c, const int32_t* slots, const int32_t* ids, int32_t n, int32_t wait,
                       void* compute_stream) {
   if (!c) return set_error(KVX_E_INVALID, "NULL cache");
-  int rc = c->check_lists(ids, slots, n);
+  int rc = c->check_lists(false, ids, slots, n);
   if (rc || n == 0) return rc;
   DeviceScope scope;
   rc = scope.enter(c->device);

@@ -91,6 +91,34 @@ def test_invalid_arguments_are_rejected_before_any_device_work():
         _lib.check(handle.kvx_sleep(None, -5))
 
 
+def test_calls_that_would_write_one_destination_twice_are_rejected():
+    # Validation runs before any device work, so these addresses are never touched.
+    handle = _lib.lib()
+    layout = layout_for(QWEN3_8B_POOL, torch.float32)
+    _, scale_off, stride = ops.entry_layout(layout, ops.FORMAT_FP8)
+    with pytest.raises(ValueError, match="appears twice in one restore"):
+        _lib.check(handle.kvx_restore_blocks(4096, ctypes.byref(layout), ops.FORMAT_FP8, _lib.int32_array([3, 5, 3]),
+                                             _lib.uint64_array([1 << 30, (1 << 30) + stride, (1 << 30) + 2 * stride]),
+                                             3, scale_off, None))
+    # Entries closer than one payload apart overlap.
+    with pytest.raises(ValueError, match="overlap"):
+        _lib.check(handle.kvx_save_blocks(4096, ctypes.byref(layout), ops.FORMAT_FP8, _lib.int32_array([3, 5]),
+                                          _lib.uint64_array([1 << 30, (1 << 30) + stride // 2]), 2, scale_off, None))
+    # One entry whose scales land inside its own payload.
+    with pytest.raises(ValueError, match="overlap"):
+        _lib.check(handle.kvx_save_blocks(4096, ctypes.byref(layout), ops.FORMAT_FP8, _lib.int32_array([3]),
+                                          _lib.uint64_array([1 << 30]), 1, 1024, None))
+    # Scales of entry 0 inside the payload of entry 1 (each entry's own ranges are disjoint).
+    with pytest.raises(ValueError, match="overlap"):
+        _lib.check(handle.kvx_save_blocks(4096, ctypes.byref(layout), ops.FORMAT_FP8, _lib.int32_array([3, 5]),
+                                          _lib.uint64_array([1 << 30, (1 << 30) + 2 * stride]), 2, 2 * stride + 4096,
+                                          None))
+    raw = layout_for(QWEN3_8B_POOL, torch.bfloat16)
+    with pytest.raises(ValueError, match="appears twice in one scatter"):
+        _lib.check(handle.kvx_scatter_tokens(4096, ctypes.byref(raw), _lib.int32_array([7, 7]), 2, 2 * 256 * 8,
+                                             1 << 30, None))
+
+
 def test_operators_refuse_cpu_tensors_instead_of_falling_back():
     x = torch.zeros((4, 128), dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="ROCm device"):

@@ -398,3 +398,24 @@ def test_coalesced_saves_and_reuse_waits_keep_victims_intact(gpu):
     for k in (keys[0], keys[2]):
         assert np.array_equal(u8(cache._entries[k].kv), expected[k]), k
     cache.close()
+
+
+def test_engine_rejects_two_copies_into_one_destination(gpu):
+    pool = make_pool(gpu, 4)
+    manager = BlockManager(4, BS)
+    keys = [publish(manager, b, 60 + b) for b in range(2)]
+    expected = block_bytes(pool, 0)
+    cache = new_cache(pool, manager, blocks=2, split_streams=True)
+    for k in keys:
+        assert cache.save_block(k)
+    slots = [cache._entries[k].slot for k in keys]
+    engine, compute = cache._engine, cache._compute_stream()
+    with pytest.raises(ValueError, match="slot appears twice"):
+        engine.save([2, 3], [slots[0], slots[0]], compute)
+    with pytest.raises(ValueError, match="block appears twice"):
+        engine.restore(slots, [3, 3], True, compute)
+    # Rejected calls queue nothing: the cache keeps working.
+    engine.restore(slots[:1], [3], True, compute)
+    cache.synchronize()
+    assert np.array_equal(block_bytes(pool, 3), expected)
+    cache.close()

@@ -127,8 +127,8 @@ def test_fp8_block_save_and_restore_match_the_oracle(gpu, geometry, scale_dtype)
     layout = ops.pool_layout(pool, scale_dtype)
     logical, offset, stride = ops.entry_layout(layout, ops.FORMAT_FP8)
     nb = pool.shape[2]
-    sources = [3, 0, nb - 1, 5]
-    dests = [1, 2, 4, nb - 2]
+    sources = list(dict.fromkeys([3, 0, nb - 1, 5]))  # distinct: one call may not name a destination twice
+    dests = list(dict.fromkeys([1, 2, 4, nb - 2]))[:len(sources)]
     staging = torch.full((len(sources) * stride,), 0xAB, dtype=torch.uint8, device=gpu)
     entries = [staging.data_ptr() + i * stride for i in range(len(sources))]
     ops.save_blocks(pool, sources, entries, ops.FORMAT_FP8, scale_dtype)
@@ -203,7 +203,8 @@ def test_bf16_block_gather_and_scatter_are_byte_exact(gpu, shape):
     layout = ops.pool_layout(pool)
     _, _, stride = ops.entry_layout(layout, ops.FORMAT_RAW)
     nb = shape[2]
-    sources, dests = [nb - 1, 0, 2], [1, 3, nb - 2]
+    dests = list(dict.fromkeys([1, 3, nb - 2]))  # distinct: one call may not name a destination twice
+    sources = [nb - 1, 0, 2][:len(dests)]
     staging = torch.zeros(len(sources) * stride, dtype=torch.uint8, device=gpu)
     entries = [staging.data_ptr() + i * stride for i in range(len(sources))]
     before = u8(pool).reshape(pool.shape + (2,))
