@@ -317,15 +317,17 @@ struct kvx_cache {
     return KVX_OK;
   }
 
-  // Saves of at most this many entry bytes per call write the pinned slots
-  // straight from the save kernel instead of staging + D2H DMA. On MI355X a
-  // D2H DMA queued behind a kernel that itself waited for another stream's
-  // event started ~0.65 ms late; one such wait per call is paid by every save
-  // call, so one-block saves (the block manager's pattern) ran at 31-40 GB/s
-  // staged against 49 GB/s written by the kernel, and a save + restore stream
-  // pair at 28 against 60 GB/s. Larger calls amortise the wait and keep the
-  // DMA (55 GB/s).
-  static constexpr int64_t kDirectSaveBytes = 256ll << 20;
+  // A one-block save has the save kernel write the pinned slot itself; larger
+  // calls gather into staging and DMA. Measured on MI355X (Qwen3-8B FP8
+  // blocks, a save and a restore stream running together):
+  //  - one block per call, staged: a D2H DMA of one entry queued behind the
+  //    save kernel, whose stream waited for a still-busy compute stream,
+  //    started ~0.65 ms late (29.6 GB/s saving, 32 GB/s both ways); written by
+  //    the kernel: 47.5 and 63 GB/s;
+  //  - 2-13 blocks per call, staged: 53-55 GB/s saving, 92-94 both ways;
+  //    written by the kernel: 49-52 and 58-66 (the kernel's host writes hold
+  //    the CUs the restore stream's kernels need).
+  static bool direct_save(int32_t n) { return n == 1; }
 
   // Copies `count` entries between consecutive staging entries and host
   // slots. Runs of consecutive slots in one slab are merged, then cut into
@@ -583,11 +585,9 @@ int kvx_cache_save(kvx_cache* c, const int32_t* ids, const int32_t* slots, int32
       }
     }
   }
-  if ((int64_t)n * c->logical_bytes_with_scales() <= kvx_cache::kDirectSaveBytes) {
-    for (int32_t base = 0; base < n; base += kMaxBatch) {
-      rc = c->launch(true, ids + base, nullptr, slots + base, std::min(kMaxBatch, n - base), s);
-      if (rc) return rc;
-    }
+  if (kvx_cache::direct_save(n)) {
+    rc = c->launch(true, ids, nullptr, slots, n, s);
+    if (rc) return rc;
   } else {
     const int32_t step = c->chunk();
     for (int32_t base = 0; base < n; base += step) {
