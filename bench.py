@@ -703,7 +703,7 @@ def main():
     dominant = "save" if k["save_ms"] >= k["restore_ms"] else "restore"
     achieved = min(save_gbs, restore_gbs)
     scale_flag = "true" if args.scale == "bf16" else "false"
-    kernel_name = (f"fp8_save_kernel<128, 2, 128, {scale_flag}>" if dominant == "save"
+    kernel_name = (f"fp8_save_kernel<128, 2, 128, {scale_flag}, false>" if dominant == "save"
                    else f"fp8_restore_kernel<128, 2, 1, {scale_flag}>")
     traffic, traffic_source = pmc_traffic(kernel_name)
     log(f"step {ms_per_step:.3f} ms; save {k['save_ms']:.3f} ms ({save_gbs:.0f} GB/s), "

@@ -139,7 +139,7 @@ static int run_batches(bool save, void* pool, const kvx_block_layout* layout, in
       b.entries[i] = entries[base + i];
     }
     const bool vec = vector_access_ok(pool, *layout, b.entries, b.n);
-    hipError_t err = save ? launch_save(pool, *layout, format, b, scale_offset, vec, stream)
+    hipError_t err = save ? launch_save(pool, *layout, format, b, scale_offset, vec, 0, stream)
                           : launch_restore(pool, *layout, format, b, scale_offset, vec, stream);
     if (err != hipSuccess) return hip_status(err, save ? "save kernel launch" : "restore kernel launch");
   }
@@ -317,17 +317,28 @@ struct kvx_cache {
     return KVX_OK;
   }
 
-  // A one-block save has the save kernel write the pinned slot itself; larger
-  // calls gather into staging and DMA. Measured on MI355X (Qwen3-8B FP8
-  // blocks, a save and a restore stream running together):
-  //  - one block per call, staged: a D2H DMA of one entry queued behind the
-  //    save kernel, whose stream waited for a still-busy compute stream,
-  //    started ~0.65 ms late (29.6 GB/s saving, 32 GB/s both ways); written by
-  //    the kernel: 47.5 and 63 GB/s;
-  //  - 2-13 blocks per call, staged: 53-55 GB/s saving, 92-94 both ways;
-  //    written by the kernel: 49-52 and 58-66 (the kernel's host writes hold
-  //    the CUs the restore stream's kernels need).
-  static bool direct_save(int32_t n) { return n == 1; }
+  // Saves of one or two blocks have the save kernel write the pinned slots
+  // itself; larger calls gather into staging and copy to the host. Measured
+  // on MI355X with Qwen3-8B FP8 blocks and a restore stream running beside
+  // the save stream (save alone / both directions, GB/s):
+  //  - staged, 1-2 blocks per call: the D2H copy of the entries, queued behind
+  //    the save kernel whose stream waited for a still-busy compute stream,
+  //    started ~0.65 ms late: 29.6 / 32 (one block), 53 / 42.5 (two blocks;
+  //    92.6 when the compute stream was idle). Three or more blocks never
+  //    showed it: 53.8-54.9 / 92.7-94.5;
+  //  - written by the kernel (grid capped, below): 51.6-52.0 / 69.4-72.8 for
+  //    one block, 52.1-52.5 / 75.3-76.4 for two, 52.5-52.8 / 76.4-76.7 for
+  //    three.
+  static bool direct_save(int32_t n) { return n <= 2; }
+
+  // Workgroups of a save that writes host slots directly. The launch lasts as
+  // long as its writes take to cross the host link (~0.4 ms per Qwen3-8B FP8
+  // block); a full grid holds every CU meanwhile and delays the restore
+  // stream's kernels. Capped at 128 workgroups, one-block calls ran at
+  // 51.5 GB/s saving alone (47.8 with the full grid) and 72 GB/s beside a
+  // restore stream (63.8); 64 workgroups saved slower (46 GB/s), 256 and more
+  // overlapped less (64-68 GB/s).
+  static constexpr int32_t kDirectSaveGrid = 128;
 
   // Copies `count` entries between consecutive staging entries and host
   // slots. Runs of consecutive slots in one slab are merged, then cut into
@@ -376,7 +387,7 @@ struct kvx_cache {
       b.entries[i] = (uint64_t)(uintptr_t)(staging ? staging + (int64_t)i * entry_stride : host_entry(slots[i]));
     }
     const bool vec = vector_access_ok(pool, layout, b.entries, b.n);
-    hipError_t err = save ? launch_save(pool, layout, format, b, scale_offset, vec, s)
+    hipError_t err = save ? launch_save(pool, layout, format, b, scale_offset, vec, staging ? 0 : kDirectSaveGrid, s)
                           : launch_restore(pool, layout, format, b, scale_offset, vec, s);
     return hip_status(err, save ? "save kernel launch" : "restore kernel launch");
   }

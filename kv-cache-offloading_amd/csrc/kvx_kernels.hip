@@ -246,9 +246,8 @@ struct TileCoord {
   int entry, plane, row0;
 };
 
-__device__ __forceinline__ TileCoord tile_coord(const PlaneGeom& g, int tile_rows) {
+__device__ __forceinline__ TileCoord tile_coord_at(const PlaneGeom& g, int tile_rows, int tile) {
   const int per_entry = g.planes * g.chunks;
-  const int tile = xcd_tile(blockIdx.x, gridDim.x);
   TileCoord t;
   t.entry = tile / per_entry;
   const int rem = tile - t.entry * per_entry;
@@ -257,11 +256,19 @@ __device__ __forceinline__ TileCoord tile_coord(const PlaneGeom& g, int tile_row
   return t;
 }
 
+__device__ __forceinline__ TileCoord tile_coord(const PlaneGeom& g, int tile_rows) {
+  return tile_coord_at(g, tile_rows, xcd_tile(blockIdx.x, gridDim.x));
+}
+
 // Save: one (token, head) row per kLanes lanes, one row per lane group; the
 // tile's codes and scales are staged in LDS so that the stores write whole
 // 128-byte lines (computing straight from the load layout leaves each store
 // instruction with half lines, which cost ~11% extra HBM write traffic).
-template <int kHd, int kVec, int kBlock, bool kScaleBf16>
+// kStride: a capped grid whose workgroups stride over the tiles, for saves
+// written straight to host memory. Such a launch lasts as long as its host
+// writes take to drain; holding only a few workgroup slots meanwhile leaves
+// the CUs to other streams' kernels (the restore stream's, say).
+template <int kHd, int kVec, int kBlock, bool kScaleBf16, bool kStride>
 __global__ __launch_bounds__(kBlock) void fp8_save_kernel(const uint16_t* __restrict__ pool, PlaneGeom g,
                                                          BlockBatch b) {
   using M = RowMap<kHd, kVec>;
@@ -270,7 +277,10 @@ __global__ __launch_bounds__(kBlock) void fp8_save_kernel(const uint16_t* __rest
   static_assert((kRows * kHd) % 16 == 0 && (kRows * kScaleBytes) % 16 == 0, "tile must store in 16-byte units");
   __shared__ uint4 codes[kRows * kHd / 16];
   __shared__ uint4 scale_tile[kRows * kScaleBytes / 16];
-  const TileCoord tc = tile_coord(g, kRows);
+  const int tiles = kStride ? b.n * g.planes * g.chunks : 1;
+  for (int tile = kStride ? (int)blockIdx.x : 0; tile < tiles; tile += kStride ? (int)gridDim.x : 1) {
+  if (kStride) __syncthreads();  // the previous tile's stores have read the LDS tile
+  const TileCoord tc = kStride ? tile_coord_at(g, kRows, tile) : tile_coord(g, kRows);
   const int lane = threadIdx.x % M::kLanes;
   const int rsub = threadIdx.x / M::kLanes;
   const int row = tc.row0 + rsub;
@@ -310,6 +320,7 @@ __global__ __launch_bounds__(kBlock) void fp8_save_kernel(const uint16_t* __rest
   } else if (lane == 0 && row < g.plane_rows) {  // ragged last tile of a plane
     if (kScaleBf16) reinterpret_cast<uint16_t*>(scales)[row] = (uint16_t)r.bits;
     else reinterpret_cast<uint32_t*>(scales)[row] = r.bits;
+  }
   }
 }
 
@@ -419,14 +430,17 @@ constexpr int kCopyVecs = 4;  // uint4 per thread per tile: 16 KiB tiles
 // Entry e receives plane p of its block at entries[e] + p * entry_plane_stride;
 // every entry copies plane_bytes per plane except the batch's last, which
 // copies last_bytes (a sequence's partial final block in a token gather).
-template <bool kToEntry>
+// kStride: a capped grid striding over the tiles, as for fp8_save_kernel.
+template <bool kToEntry, bool kStride>
 __global__ __launch_bounds__(kThreads) void raw_copy_kernel(uint8_t* __restrict__ pool, PlaneGeom g,
                                                            BlockBatch b, int64_t plane_bytes,
                                                            int64_t elem_bytes, int64_t entry_plane_stride,
                                                            int64_t last_bytes) {
   constexpr int kTileBytes = kThreads * kCopyVecs * 16;
   const int per_entry = g.planes * g.chunks;
-  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  const int tiles = kStride ? b.n * per_entry : 1;
+  for (int t = kStride ? (int)blockIdx.x : 0; t < tiles; t += kStride ? (int)gridDim.x : 1) {
+  const int tile = kStride ? t : xcd_tile(blockIdx.x, gridDim.x);
   const int e = tile / per_entry;
   const int rem = tile - e * per_entry;
   const int p = rem / g.chunks;
@@ -446,6 +460,7 @@ __global__ __launch_bounds__(kThreads) void raw_copy_kernel(uint8_t* __restrict_
   for (int k = 0; k < kCopyVecs; ++k) {
     const int64_t off = off0 + ((int64_t)k * kThreads + threadIdx.x) * 16;
     if (off < valid) store_nt16(dst + off, v[k]);
+  }
   }
 }
 
@@ -618,29 +633,37 @@ static unsigned generic_grid(int64_t items) { return (unsigned)((items + kThread
 
 template <bool kScaleBf16>
 static hipError_t launch_fp8(bool save, void* pool, const kvx_block_layout& l, const BlockBatch& b,
-                             int64_t scale_offset, bool vector_ok, hipStream_t stream) {
+                             int64_t scale_offset, bool vector_ok, int32_t max_grid, hipStream_t stream) {
   // Tile shapes chosen by sweeps on the Qwen3-8B block workload: restore
   // 256 threads x 1 pass (32 rows for hd=128), save 128 threads (16 rows).
   constexpr int kPasses = 1;
   constexpr int kSaveBlock = 128;
-  auto run = [&](auto save_k, auto restore_k, int lanes) -> hipError_t {
+  auto run = [&](auto save_k, auto save_stride_k, auto restore_k, int lanes) -> hipError_t {
     const int tile = save ? kSaveBlock / lanes : (kThreads / lanes) * kPasses;
     PlaneGeom g = make_geom(l, tile, scale_offset);
     const unsigned grid = (unsigned)(b.n * g.planes * g.chunks);
-    if (save) hipLaunchKernelGGL(save_k, dim3(grid), dim3(kSaveBlock), 0, stream, (const uint16_t*)pool, g, b);
-    else hipLaunchKernelGGL(restore_k, dim3(grid), dim3(kThreads), 0, stream, (uint16_t*)pool, g, b);
+    if (save && max_grid > 0 && (unsigned)max_grid < grid)
+      hipLaunchKernelGGL(save_stride_k, dim3((unsigned)max_grid), dim3(kSaveBlock), 0, stream, (const uint16_t*)pool,
+                         g, b);
+    else if (save)
+      hipLaunchKernelGGL(save_k, dim3(grid), dim3(kSaveBlock), 0, stream, (const uint16_t*)pool, g, b);
+    else
+      hipLaunchKernelGGL(restore_k, dim3(grid), dim3(kThreads), 0, stream, (uint16_t*)pool, g, b);
     return hipGetLastError();
   };
   switch (vector_ok ? l.head_dim : 0) {
     case 64:
-      return run(fp8_save_kernel<64, 1, kSaveBlock, kScaleBf16>, fp8_restore_kernel<64, 1, kPasses, kScaleBf16>,
-                 RowMap<64, 1>::kLanes);
+      return run(fp8_save_kernel<64, 1, kSaveBlock, kScaleBf16, false>,
+                 fp8_save_kernel<64, 1, kSaveBlock, kScaleBf16, true>,
+                 fp8_restore_kernel<64, 1, kPasses, kScaleBf16>, RowMap<64, 1>::kLanes);
     case 128:
-      return run(fp8_save_kernel<128, 2, kSaveBlock, kScaleBf16>, fp8_restore_kernel<128, 2, kPasses, kScaleBf16>,
-                 RowMap<128, 2>::kLanes);
+      return run(fp8_save_kernel<128, 2, kSaveBlock, kScaleBf16, false>,
+                 fp8_save_kernel<128, 2, kSaveBlock, kScaleBf16, true>,
+                 fp8_restore_kernel<128, 2, kPasses, kScaleBf16>, RowMap<128, 2>::kLanes);
     case 256:
-      return run(fp8_save_kernel<256, 2, kSaveBlock, kScaleBf16>, fp8_restore_kernel<256, 2, kPasses, kScaleBf16>,
-                 RowMap<256, 2>::kLanes);
+      return run(fp8_save_kernel<256, 2, kSaveBlock, kScaleBf16, false>,
+                 fp8_save_kernel<256, 2, kSaveBlock, kScaleBf16, true>,
+                 fp8_restore_kernel<256, 2, kPasses, kScaleBf16>, RowMap<256, 2>::kLanes);
     default: {
       PlaneGeom g = make_geom(l, 0, scale_offset);
       const unsigned grid = generic_grid((int64_t)b.n * l.planes * l.plane_rows);
@@ -656,7 +679,8 @@ static hipError_t launch_fp8(bool save, void* pool, const kvx_block_layout& l, c
 }
 
 static hipError_t launch_raw(bool to_entry, void* pool, const kvx_block_layout& l, const BlockBatch& b,
-                             bool vector_ok, int64_t entry_plane_stride, int64_t last_bytes, hipStream_t stream) {
+                             bool vector_ok, int64_t entry_plane_stride, int64_t last_bytes, int32_t max_grid,
+                             hipStream_t stream) {
   const int64_t plane_bytes = (int64_t)l.plane_rows * l.head_dim * l.elem_bytes;
   if (entry_plane_stride < 0) entry_plane_stride = plane_bytes;
   if (last_bytes < 0) last_bytes = plane_bytes;
@@ -667,12 +691,15 @@ static hipError_t launch_raw(bool to_entry, void* pool, const kvx_block_layout& 
     PlaneGeom g = make_geom(l, 0, 0);
     g.chunks = (int32_t)((plane_bytes + kTileBytes - 1) / kTileBytes);
     const unsigned grid = (unsigned)(b.n * g.planes * g.chunks);
-    if (to_entry)
-      hipLaunchKernelGGL(raw_copy_kernel<true>, dim3(grid), dim3(kThreads), 0, stream, (uint8_t*)pool, g, b,
+    if (to_entry && max_grid > 0 && (unsigned)max_grid < grid)
+      hipLaunchKernelGGL((raw_copy_kernel<true, true>), dim3((unsigned)max_grid), dim3(kThreads), 0, stream,
+                         (uint8_t*)pool, g, b, plane_bytes, es, entry_plane_stride, last_bytes);
+    else if (to_entry)
+      hipLaunchKernelGGL((raw_copy_kernel<true, false>), dim3(grid), dim3(kThreads), 0, stream, (uint8_t*)pool, g, b,
                          plane_bytes, es, entry_plane_stride, last_bytes);
     else
-      hipLaunchKernelGGL(raw_copy_kernel<false>, dim3(grid), dim3(kThreads), 0, stream, (uint8_t*)pool, g, b,
-                         plane_bytes, es, entry_plane_stride, last_bytes);
+      hipLaunchKernelGGL((raw_copy_kernel<false, false>), dim3(grid), dim3(kThreads), 0, stream, (uint8_t*)pool, g,
+                         b, plane_bytes, es, entry_plane_stride, last_bytes);
   } else {
     PlaneGeom g = make_geom(l, 0, 0);
     const unsigned grid = generic_grid((int64_t)b.n * l.planes * (plane_bytes / 2));
@@ -689,7 +716,7 @@ static hipError_t launch_raw(bool to_entry, void* pool, const kvx_block_layout& 
 hipError_t launch_token_copy(bool gather, void* pool, const kvx_block_layout& l, const BlockBatch& b,
                              bool vector_ok, int64_t dense_plane_stride, int64_t last_bytes, hipStream_t stream) {
   if (b.n <= 0) return hipSuccess;
-  return launch_raw(gather, pool, l, b, vector_ok, dense_plane_stride, last_bytes, stream);
+  return launch_raw(gather, pool, l, b, vector_ok, dense_plane_stride, last_bytes, 0, stream);
 }
 
 bool vector_access_ok(const void* pool, const kvx_block_layout& l, const uint64_t* entries, int32_t n) {
@@ -701,20 +728,21 @@ bool vector_access_ok(const void* pool, const kvx_block_layout& l, const uint64_
 }
 
 hipError_t launch_save(const void* pool, const kvx_block_layout& l, int32_t format, const BlockBatch& b,
-                       int64_t scale_offset, bool vector_ok, hipStream_t stream) {
+                       int64_t scale_offset, bool vector_ok, int32_t max_grid, hipStream_t stream) {
   if (b.n <= 0) return hipSuccess;
   void* p = const_cast<void*>(pool);
-  if (format == KVX_FORMAT_RAW) return launch_raw(true, p, l, b, vector_ok, -1, -1, stream);
-  return l.scale_dtype == KVX_SCALE_BF16 ? launch_fp8<true>(true, p, l, b, scale_offset, vector_ok, stream)
-                                         : launch_fp8<false>(true, p, l, b, scale_offset, vector_ok, stream);
+  if (format == KVX_FORMAT_RAW) return launch_raw(true, p, l, b, vector_ok, -1, -1, max_grid, stream);
+  return l.scale_dtype == KVX_SCALE_BF16
+             ? launch_fp8<true>(true, p, l, b, scale_offset, vector_ok, max_grid, stream)
+             : launch_fp8<false>(true, p, l, b, scale_offset, vector_ok, max_grid, stream);
 }
 
 hipError_t launch_restore(void* pool, const kvx_block_layout& l, int32_t format, const BlockBatch& b,
                           int64_t scale_offset, bool vector_ok, hipStream_t stream) {
   if (b.n <= 0) return hipSuccess;
-  if (format == KVX_FORMAT_RAW) return launch_raw(false, pool, l, b, vector_ok, -1, -1, stream);
-  return l.scale_dtype == KVX_SCALE_BF16 ? launch_fp8<true>(false, pool, l, b, scale_offset, vector_ok, stream)
-                                         : launch_fp8<false>(false, pool, l, b, scale_offset, vector_ok, stream);
+  if (format == KVX_FORMAT_RAW) return launch_raw(false, pool, l, b, vector_ok, -1, -1, 0, stream);
+  return l.scale_dtype == KVX_SCALE_BF16 ? launch_fp8<true>(false, pool, l, b, scale_offset, vector_ok, 0, stream)
+                                         : launch_fp8<false>(false, pool, l, b, scale_offset, vector_ok, 0, stream);
 }
 
 hipError_t launch_store_kvcache(const void* key, int64_t key_stride, const void* value, int64_t value_stride,

@@ -419,3 +419,44 @@ def test_engine_rejects_two_copies_into_one_destination(gpu):
     cache.synchronize()
     assert np.array_equal(block_bytes(pool, 3), expected)
     cache.close()
+
+
+@pytest.mark.parametrize("fmt,scale_dtype", [(ops.FORMAT_FP8, torch.float32), (ops.FORMAT_FP8, torch.bfloat16),
+                                             (ops.FORMAT_RAW, None)])
+def test_engine_saves_of_every_path_write_the_oracle_bytes(gpu, fmt, scale_dtype):
+    # Calls of 1-2 blocks are written to the host slots by a capped grid of save workgroups that stride over
+    # the tiles; 3+ blocks go through staging and a copy. A 48-token block of 3 layers has 144 tiles, which
+    # 128 striding workgroups do not divide evenly.
+    from kvx.engine.cpu_prefix_cache import _CopyEngine
+
+    g = torch.Generator(device=gpu).manual_seed(11)
+    pool = (torch.randn((2, 3, 9, 48, 8, 128), generator=g, device=gpu) * 3).to(torch.bfloat16)
+    layout = ops.pool_layout(pool, scale_dtype)
+    engine = _CopyEngine(pool, layout, fmt, split=True)
+    try:
+        stride = engine.entry_stride
+        slab = torch.full((8 * stride,), 0xA5, dtype=torch.uint8, pin_memory=True)
+        staging = [torch.empty(4 * stride, dtype=torch.uint8, device=gpu) for _ in range(2)]
+        engine.add_slab(slab, 8)
+        engine.set_staging(*staging, 4)
+        compute = torch.cuda.current_stream(gpu).cuda_stream
+        calls = [([7], [0]), ([2, 5], [1, 2]), ([0, 8, 3], [3, 4, 5]), ([1, 6], [7, 6])]
+        for blocks, slots in calls:
+            engine.save(blocks, slots, compute)
+        engine.synchronize()
+        host_pool = bf16_bits(pool)
+        entries = slab.numpy().reshape(8, stride)
+        for blocks, slots in calls:
+            for b, slot in zip(blocks, slots):
+                got = entries[slot]
+                if fmt == ops.FORMAT_RAW:
+                    want = np.ascontiguousarray(host_pool[:, :, b]).view(np.uint8).ravel()
+                    assert np.array_equal(got[:want.size], want), (b, slot)
+                    continue
+                codes, scales = oracle.save_block_fp8(host_pool, b, scale_dtype == torch.float32)
+                offset = engine.scale_offset
+                assert np.array_equal(got[:codes.size], codes.ravel()), (b, slot)
+                assert np.array_equal(got[offset:offset + scales.nbytes], scales.view(np.uint8).ravel()), (b, slot)
+        assert engine.counters()["saved_blocks"] == 8
+    finally:
+        engine.close()
