@@ -177,13 +177,20 @@ class _CopyBatcher:
     no work that reads or writes those blocks may be queued on the caller's
     stream inside it. Anything that must follow a held-back copy flushes
     first: a save of a block a held-back restore writes, a save into a slot a
-    held-back restore reads or a held-back save writes, before_block_use or
-    before_block_reuse of a block with a held-back restore.
+    held-back restore reads or a held-back save writes, a restore into a block
+    a held-back restore writes, before_block_use or before_block_reuse of a
+    block with a held-back restore.
+
+    Callers publish a held-back copy's metadata when they queue it. If a flush
+    fails (the engine validates its arguments before queuing anything, so only
+    a HIP error can), `on_failure(saves, restores)` gets every copy of that
+    flush, whether or not it was issued, so the caller can withdraw them.
     """
 
-    def __init__(self, engine, compute_stream):
+    def __init__(self, engine, compute_stream, on_failure=None):
         self.engine = engine
         self._compute = compute_stream  # () -> the caller's current stream handle
+        self._on_failure = on_failure
         self.depth = 0
         self.saves: list[tuple[int, int]] = []  # (block, slot)
         self.save_slots: set[int] = set()
@@ -202,6 +209,8 @@ class _CopyBatcher:
         self.engine.save([block_id], [slot], self._compute())
 
     def restore(self, slot: int, block_id: int, wait: bool):
+        if block_id in self.restore_blocks:
+            self.flush()
         if self.depth:
             self.restores.append((slot, block_id, wait))
             self.restore_blocks.add(block_id)
@@ -237,19 +246,24 @@ class _CopyBatcher:
         reuse, self.reuse = self.reuse, []
         restores, self.restores = self.restores, []
         self.restore_blocks, self.restore_slots = set(), set()
-        compute = self._compute()
-        if saves:
-            self.engine.save([block for block, _ in saves], [slot for _, slot in saves], compute)
-        for block_id in reuse:
-            self.engine.before_block_reuse(block_id, compute)
-        start = 0
-        while start < len(restores):
-            end, wait = start, restores[start][2]
-            while end < len(restores) and restores[end][2] == wait:
-                end += 1
-            run = restores[start:end]
-            self.engine.restore([slot for slot, _, _ in run], [block for _, block, _ in run], wait, compute)
-            start = end
+        try:
+            compute = self._compute()
+            if saves:
+                self.engine.save([block for block, _ in saves], [slot for _, slot in saves], compute)
+            for block_id in reuse:
+                self.engine.before_block_reuse(block_id, compute)
+            start = 0
+            while start < len(restores):
+                end, wait = start, restores[start][2]
+                while end < len(restores) and restores[end][2] == wait:
+                    end += 1
+                run = restores[start:end]
+                self.engine.restore([slot for slot, _, _ in run], [block for _, block, _ in run], wait, compute)
+                start = end
+        except BaseException:
+            if self._on_failure is not None and (saves or restores):
+                self._on_failure(saves, restores)
+            raise
 
 
 class CPUBlockCache:
@@ -326,7 +340,7 @@ class CPUBlockCache:
         self._copy_stream = self._engine.save_stream
         self._restore_stream = self._engine.restore_stream
         self._staging: list[torch.Tensor] = []
-        self._batcher = _CopyBatcher(self._engine, self._compute_stream)
+        self._batcher = _CopyBatcher(self._engine, self._compute_stream, self._withdraw_copies)
         if automatic:
             if block_manager._cpu_prefix_cache is not None:
                 self._engine.close()
@@ -507,6 +521,21 @@ class CPUBlockCache:
         """Batch the saves and restores issued inside a `with` block (see _CopyBatcher); used by the block
         manager's admission, prefetch and release loops."""
         return self._batcher.coalesce()
+
+    def _withdraw_copies(self, saves, restores):
+        """A batch of held-back copies failed to issue: drop the CPU entries its saves published and unpublish
+        the GPU blocks its restores filled, so no metadata names bytes that may never have been copied."""
+        slots = {slot for _, slot in saves}
+        for prefix_hash in [h for h, e in self._entries.items() if e.slot in slots]:
+            self._free_slots.append(self._entries.pop(prefix_hash).slot)
+            self._saved_blocks -= 1
+        manager = self._manager
+        for _, block_id, _ in restores:
+            block = manager.blocks[block_id]
+            if block.hash != -1 and manager.hash_to_block_id.get(block.hash) == block_id:
+                del manager.hash_to_block_id[block.hash]
+            block.hash, block.token_ids = -1, []
+            self._restored_blocks -= 1
 
     def save_block(self, prefix_hash: int) -> bool:
         """Save a published full block; return False if already saved (cpu_prefix_cache.py:275-332).

@@ -88,6 +88,8 @@ def test_reuse_wait_without_held_back_saves_is_immediate():
     ("save into a slot a held-back restore reads", lambda b: b.save(3, 10), ("save", [3], [10])),
     ("save into a slot a held-back save writes", lambda b: b.save(3, 20), ("save", [3], [20])),
     ("use of a block a held-back restore writes", lambda b: b.before_block_use(2), ("use", 2)),
+    ("restore into a block a held-back restore writes", lambda b: b.restore(11, 2, False),
+     ("restore", [11], [2], False)),
     ("reuse of a block a held-back restore writes", lambda b: b.before_block_reuse(2), ("reuse", 2)),
 ])
 def test_conflicts_flush_first(conflict, call, after):
@@ -97,8 +99,8 @@ def test_conflicts_flush_first(conflict, call, after):
         batcher.save(1, 20)
         batcher.restore(10, 2, True)
         call(batcher)
-        # The conflicting call comes after the flush; a save is held back again until the block ends.
-        assert engine.calls == flushed + ([] if after[0] == "save" else [after]), conflict
+        # The conflicting call comes after the flush; a copy is held back again until the block ends.
+        assert engine.calls == flushed + ([] if after[0] in ("save", "restore") else [after]), conflict
     assert engine.calls == flushed + [after], conflict
 
 
@@ -132,4 +134,26 @@ def test_exception_inside_the_block_still_issues_queued_copies():
     assert engine.calls == [("save", [1], [20]), ("restore", [10], [2], True)]
     assert batcher.depth == 0
     batcher.save(4, 21)  # back to immediate calls
+    assert engine.calls[-1] == ("save", [4], [21])
+
+
+class FailingEngine(RecordingEngine):
+    def restore(self, slots, blocks, wait, stream):
+        raise RuntimeError("hipErrorLaunchFailure")
+
+
+def test_a_failed_flush_reports_every_copy_of_it_and_raises():
+    engine = FailingEngine()
+    failed = []
+    batcher = _CopyBatcher(engine, lambda: STREAM, lambda saves, restores: failed.append((saves, restores)))
+    with pytest.raises(RuntimeError, match="LaunchFailure"):
+        with batcher.coalesce():
+            batcher.save(1, 20)
+            batcher.restore(10, 2, True)
+            batcher.restore(11, 3, False)
+    # The save was issued before the restore failed; it is reported too (the caller cannot tell).
+    assert engine.calls == [("save", [1], [20])]
+    assert failed == [([(1, 20)], [(10, 2, True), (11, 3, False)])]
+    assert batcher.depth == 0 and not (batcher.saves or batcher.restores or batcher.restore_blocks)
+    batcher.save(4, 21)  # the batcher is usable again
     assert engine.calls[-1] == ("save", [4], [21])

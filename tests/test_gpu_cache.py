@@ -460,3 +460,34 @@ def test_engine_saves_of_every_path_write_the_oracle_bytes(gpu, fmt, scale_dtype
         assert engine.counters()["saved_blocks"] == 8
     finally:
         engine.close()
+
+
+def test_a_failed_batch_withdraws_the_metadata_it_published(gpu, monkeypatch):
+    pool = make_pool(gpu, 6)
+    manager = BlockManager(6, BS)
+    keys = [publish(manager, b, 70 + b) for b in range(2)]
+    expected = block_bytes(pool, 0)
+    cache = new_cache(pool, manager, blocks=3, split_streams=True)
+    assert cache.save_block(keys[0])
+    cache.synchronize()
+    forget(manager, keys[0])  # only the CPU copy of keys[0] remains
+
+    def broken(*args):
+        raise RuntimeError("hipErrorLaunchFailure")
+
+    engine_restore = cache._engine.restore
+    monkeypatch.setattr(cache._engine, "restore", broken)
+    with pytest.raises(RuntimeError, match="LaunchFailure"):
+        with cache.coalesce():
+            assert cache.save_block(keys[1])  # published now, issued at the end of the block
+            target = cache.restore_block(keys[0])  # published now, issued at the end of the block
+            assert keys[1] in cache._entries and manager.hash_to_block_id.get(keys[0]) == target
+    # Neither the save nor the restore may be trusted: both are withdrawn.
+    assert keys[1] not in cache._entries
+    assert keys[0] not in manager.hash_to_block_id and manager.blocks[target].hash == -1
+    assert keys[0] in cache._entries  # the CPU copy that was already saved stays for a retry
+    monkeypatch.setattr(cache._engine, "restore", engine_restore)
+    again = cache.restore_block(keys[0])
+    cache.synchronize()
+    assert np.array_equal(block_bytes(pool, again), expected)
+    cache.close()
