@@ -54,6 +54,7 @@ def parse_args():
     p.add_argument("--skip-hybrid", action="store_true", help="skip the hybrid-admission calibration leg")
     p.add_argument("--skip-agents", action="store_true", help="skip the agent-pressure leg")
     p.add_argument("--skip-handoff", action="store_true", help="skip the KV handoff leg")
+    p.add_argument("--skip-microbench", action="store_true", help="skip the copy-path microbenchmark leg")
     p.add_argument("--skip-reference-gpu", action="store_true",
                    help="skip timing the reference's torch codec chain on the GPU")
     p.add_argument("--skip-configs", action="store_true",
@@ -183,6 +184,123 @@ def store_leg(torch, ops, pool, reps=5):
     out["paged_blocks"] = {"tokens": pos, "ms_all_layers": round(1000 * t, 4),
                            "algorithmic_bytes_per_launch": per_launch, "hbm_gbs": round(gbs, 1),
                            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    return out
+
+
+def microbench_leg(torch, blocks=64, matmul_iters=200):
+    """The reference's copy-path microbenchmark (bench/cpu_cache_microbench.py:59-163) on this path.
+
+    Same workload and measurements: a Qwen3-0.6B-shaped pool of 2 * blocks
+    blocks; pinned memcpy ceilings (:91-98); the cost of a pinned allocation
+    per save (:101-106) and of a synchronous pageable save (:109-116); per-block
+    save_block / restore_block through the cache (:119-127); and whether saves
+    on the copy stream slow concurrent compute, 4096^2 bf16 matmuls (:130-155).
+    Issue time is host time until the calls return, total adds the device wait.
+    The reference runs its default (BF16) cache; the FP8 cache runs as well.
+    """
+    from types import SimpleNamespace
+
+    from kvx.engine.block_manager import BlockManager
+    from kvx.engine.cpu_prefix_cache import CPUBlockCache
+    from kvx.workloads import QWEN3_0_6B
+
+    n = blocks
+    shape = (2, QWEN3_0_6B.layers, 2 * n, *QWEN3_0_6B.shape[3:])
+    g = torch.Generator(device="cuda").manual_seed(0)
+    pool = torch.randn(shape, generator=g, device="cuda").to(torch.bfloat16)
+    bs = shape[3]
+    block_shape = (2, shape[1], *shape[3:])
+    block_bytes = pool[:, :, 0].numel() * pool.element_size()
+    runner = SimpleNamespace(world_size=1, block_size=bs, kv_cache=pool)
+
+    def timed(fn):
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        fn()
+        issued = time.perf_counter()
+        torch.cuda.synchronize()
+        return issued - start, time.perf_counter() - start
+
+    def per_block(issue_s, total_s, nbytes=block_bytes):
+        return {"issue_ms_per_block": round(1000 * issue_s / n, 4), "ms_per_block": round(1000 * total_s / n, 4),
+                "gb_per_s": round(n * nbytes / total_s / 1e9, 2)}
+
+    def published():
+        manager = BlockManager(2 * n, bs)
+        hashes = []
+        for i in range(n):
+            tokens = [i] * bs
+            h = BlockManager.compute_hash(tokens)
+            manager.blocks[i].update(h, tokens)
+            manager.hash_to_block_id[h] = i
+            hashes.append(h)
+        return manager, hashes
+
+    out = {"pool": list(shape), "blocks": n, "block_bytes": block_bytes}
+    flat_gpu = torch.empty(n * block_bytes // 2, dtype=torch.bfloat16, device="cuda")
+    flat_host = torch.empty_like(flat_gpu, device="cpu", pin_memory=True)
+    flat_host.copy_(flat_gpu)
+    out["pinned_memcpy_d2h"] = per_block(*timed(lambda: flat_host.copy_(flat_gpu, non_blocking=True)))
+    out["pinned_memcpy_h2d"] = per_block(*timed(lambda: flat_gpu.copy_(flat_host, non_blocking=True)))
+    del flat_gpu, flat_host
+
+    def pinned_allocs():
+        return [torch.empty(block_shape, dtype=pool.dtype, pin_memory=True) for _ in range(n)]
+
+    _, total = timed(pinned_allocs)
+    out["per_save_pinned_alloc"] = {"ms_per_block": round(1000 * total / n, 4)}
+
+    def pageable_saves():
+        keep = []
+        for i in range(n):
+            payload = torch.empty(block_shape, dtype=pool.dtype)
+            torch.cuda.synchronize()
+            payload.copy_(pool[:, :, i], non_blocking=False)
+            keep.append(payload)
+
+    out["pageable_sync_save"] = per_block(*timed(pageable_saves))
+
+    x = torch.randn(4096, 4096, dtype=torch.bfloat16, device="cuda")
+
+    def matmuls():
+        for _ in range(matmul_iters):
+            torch.mm(x, x)
+
+    matmuls()  # library warm-up
+    _, compute_s = timed(matmuls)
+    for name, fp8 in (("bf16", False), ("fp8", True)):
+        manager, hashes = published()
+        kw = dict(fp8=True, scale_dtype=torch.float32) if fp8 else {}
+        start = time.perf_counter()
+        cache = CPUBlockCache(runner, manager, n * block_bytes, preallocate=True, **kw)
+        res = {"slab_preallocate_s": round(time.perf_counter() - start, 3)}
+        entry = cache.block_bytes
+        try:
+            res["slab_save"] = per_block(*timed(lambda: [cache.save_block(h) for h in hashes]), entry)
+            for h in hashes:
+                block = manager.blocks[manager.hash_to_block_id.pop(h)]
+                block.hash, block.token_ids = -1, []
+            res["slab_restore"] = per_block(*timed(lambda: [cache.restore_block(h) for h in hashes]), entry)
+        finally:
+            cache.close()
+        manager, hashes = published()
+        cache = CPUBlockCache(runner, manager, n * block_bytes, preallocate=True, **kw)
+        try:
+            _, copy_s = timed(lambda: [cache.save_block(h) for h in hashes])
+            cache.clear()
+
+            def both():
+                for h in hashes:  # saves first: each waits for the compute queued before it
+                    cache.save_block(h)
+                matmuls()
+
+            _, both_s = timed(both)
+        finally:
+            cache.close()
+        res["overlap"] = {"compute_alone_s": round(compute_s, 5), "saves_alone_s": round(copy_s, 5),
+                          "together_s": round(both_s, 5), "serial_sum_s": round(compute_s + copy_s, 5),
+                          "hidden_fraction": round((compute_s + copy_s - both_s) / min(compute_s, copy_s), 3)}
+        out[name] = res
     return out
 
 
@@ -782,6 +900,9 @@ def main():
     if not args.skip_handoff:
         log("kv handoff leg")
         result["kv_handoff"] = handoff_leg(torch, pool)
+    if not args.skip_microbench:
+        log("copy-path microbench leg")
+        result["microbench"] = microbench_leg(torch)
     if not args.skip_hybrid:
         log("hybrid calibration leg")
         result["hybrid_admission"] = hybrid_leg(torch, pool, scale_dtype)

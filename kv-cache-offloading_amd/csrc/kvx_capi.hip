@@ -326,19 +326,21 @@ struct kvx_cache {
   //    started ~0.65 ms late: 29.6 / 32 (one block), 53 / 42.5 (two blocks;
   //    92.6 when the compute stream was idle). Three or more blocks never
   //    showed it: 53.8-54.9 / 92.7-94.5;
-  //  - written by the kernel (grid capped, below): 51.6-52.0 / 69.4-72.8 for
-  //    one block, 52.1-52.5 / 75.3-76.4 for two, 52.5-52.8 / 76.4-76.7 for
-  //    three.
+  //  - written by the kernel (direct_save_grid workgroups, system-scope
+  //    stores): 48.7-48.8 / 93.0 for one block, 49.5 / 93.5-93.8 for two.
   static bool direct_save(int32_t n) { return n <= 2; }
 
   // Workgroups of a save that writes host slots directly. The launch lasts as
   // long as its writes take to cross the host link (~0.4 ms per Qwen3-8B FP8
-  // block); a full grid holds every CU meanwhile and delays the restore
-  // stream's kernels. Capped at 128 workgroups, one-block calls ran at
-  // 51.5 GB/s saving alone (47.8 with the full grid) and 72 GB/s beside a
-  // restore stream (63.8); 64 workgroups saved slower (46 GB/s), 256 and more
-  // overlapped less (64-68 GB/s).
-  static constexpr int32_t kDirectSaveGrid = 128;
+  // block). Too many workgroups hold CUs the restore stream's kernels need
+  // and crowd the link's upstream direction, which also carries the restore
+  // DMA's read requests; too few cannot keep the link busy. Measured for
+  // one-block saves beside one-block restores (save alone / both, GB/s):
+  //   FP8 (2 KiB tiles): 16 -> 25 / 49, 24 -> 37 / 72, 32 -> 48.6 / 92.8,
+  //                      48 -> 53.8 / 86, 64 -> 52.9 / 76, 128 -> 53.4 / 77;
+  //   BF16 (16 KiB tiles): 16 -> 55.4 / 90.3, 24 -> 55.9 / 87.8,
+  //                        32 -> 54.5 / 85, 64 -> 56 / 82.4.
+  int32_t direct_save_grid() const { return format == KVX_FORMAT_FP8 ? 32 : 16; }
 
   // Copies `count` entries between consecutive staging entries and host
   // slots. Runs of consecutive slots in one slab are merged, then cut into
@@ -387,7 +389,7 @@ struct kvx_cache {
       b.entries[i] = (uint64_t)(uintptr_t)(staging ? staging + (int64_t)i * entry_stride : host_entry(slots[i]));
     }
     const bool vec = vector_access_ok(pool, layout, b.entries, b.n);
-    hipError_t err = save ? launch_save(pool, layout, format, b, scale_offset, vec, staging ? 0 : kDirectSaveGrid, s)
+    hipError_t err = save ? launch_save(pool, layout, format, b, scale_offset, vec, staging ? 0 : direct_save_grid(), s)
                           : launch_restore(pool, layout, format, b, scale_offset, vec, s);
     return hip_status(err, save ? "save kernel launch" : "restore kernel launch");
   }

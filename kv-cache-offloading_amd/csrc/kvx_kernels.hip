@@ -43,6 +43,23 @@ __device__ __forceinline__ void store_nt16(void* p, uint4 v) {
   __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(p));
 }
 
+// A 16-byte vector store with system scope (sc0 sc1: written through to
+// memory, as host memory must be), for kernels that write pinned host slots.
+// Measured on MI355X with one-block FP8 saves from 128 workgroups running
+// beside a restore stream: 77 GB/s both ways against 71 with nontemporal
+// stores, and concurrent bf16 matmuls took 1.4x their time alone instead of
+// 1.7x.
+__device__ __forceinline__ void store_host16(void* p, uint4 v) {
+  u32x4 w = {v.x, v.y, v.z, v.w};
+  asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1" : : "v"(p), "v"(w) : "memory");
+}
+
+template <bool kHost>
+__device__ __forceinline__ void store16(void* p, uint4 v) {
+  if (kHost) store_host16(p, v);
+  else store_nt16(p, v);
+}
+
 // Workgroups are dispatched round-robin over the chip's 8 XCDs, each with its
 // own L2. Handing each XCD a contiguous range of tiles (instead of every 8th
 // tile) keeps every XCD streaming through one region of memory; on the
@@ -264,10 +281,10 @@ __device__ __forceinline__ TileCoord tile_coord(const PlaneGeom& g, int tile_row
 // tile's codes and scales are staged in LDS so that the stores write whole
 // 128-byte lines (computing straight from the load layout leaves each store
 // instruction with half lines, which cost ~11% extra HBM write traffic).
-// kStride: a capped grid whose workgroups stride over the tiles, for saves
-// written straight to host memory. Such a launch lasts as long as its host
-// writes take to drain; holding only a few workgroup slots meanwhile leaves
-// the CUs to other streams' kernels (the restore stream's, say).
+// kStride: saves written straight to host memory, by a capped grid whose
+// workgroups stride over the tiles, with system-scope stores. Such a launch
+// lasts as long as its writes take to cross the host link; a few workgroups
+// keep the link busy and leave the CUs to other streams' kernels.
 template <int kHd, int kVec, int kBlock, bool kScaleBf16, bool kStride>
 __global__ __launch_bounds__(kBlock) void fp8_save_kernel(const uint16_t* __restrict__ pool, PlaneGeom g,
                                                          BlockBatch b) {
@@ -313,10 +330,10 @@ __global__ __launch_bounds__(kBlock) void fp8_save_kernel(const uint16_t* __rest
   __syncthreads();
   uint8_t* tile_payload = payload + (int64_t)tc.row0 * kHd;
   for (int i = threadIdx.x; i < kRows * kHd / 16; i += kBlock)
-    if (full || tc.row0 + i * 16 / kHd < g.plane_rows) store_nt16(tile_payload + i * 16, codes[i]);
+    if (full || tc.row0 + i * 16 / kHd < g.plane_rows) store16<kStride>(tile_payload + i * 16, codes[i]);
   if (full) {
     for (int i = threadIdx.x; i < kRows * kScaleBytes / 16; i += kBlock)
-      store_nt16(scales + (int64_t)tc.row0 * kScaleBytes + i * 16, scale_tile[i]);
+      store16<kStride>(scales + (int64_t)tc.row0 * kScaleBytes + i * 16, scale_tile[i]);
   } else if (lane == 0 && row < g.plane_rows) {  // ragged last tile of a plane
     if (kScaleBf16) reinterpret_cast<uint16_t*>(scales)[row] = (uint16_t)r.bits;
     else reinterpret_cast<uint32_t*>(scales)[row] = r.bits;
@@ -430,7 +447,8 @@ constexpr int kCopyVecs = 4;  // uint4 per thread per tile: 16 KiB tiles
 // Entry e receives plane p of its block at entries[e] + p * entry_plane_stride;
 // every entry copies plane_bytes per plane except the batch's last, which
 // copies last_bytes (a sequence's partial final block in a token gather).
-// kStride: a capped grid striding over the tiles, as for fp8_save_kernel.
+// kStride: saves to host memory (capped striding grid, system-scope stores),
+// as for fp8_save_kernel.
 template <bool kToEntry, bool kStride>
 __global__ __launch_bounds__(kThreads) void raw_copy_kernel(uint8_t* __restrict__ pool, PlaneGeom g,
                                                            BlockBatch b, int64_t plane_bytes,
@@ -459,7 +477,7 @@ __global__ __launch_bounds__(kThreads) void raw_copy_kernel(uint8_t* __restrict_
 #pragma unroll
   for (int k = 0; k < kCopyVecs; ++k) {
     const int64_t off = off0 + ((int64_t)k * kThreads + threadIdx.x) * 16;
-    if (off < valid) store_nt16(dst + off, v[k]);
+    if (off < valid) store16<kStride>(dst + off, v[k]);
   }
   }
 }
