@@ -421,16 +421,17 @@ def test_engine_rejects_two_copies_into_one_destination(gpu):
     cache.close()
 
 
+@pytest.mark.parametrize("heads,hd", [(8, 128), (4, 64), (2, 256)])
 @pytest.mark.parametrize("fmt,scale_dtype", [(ops.FORMAT_FP8, torch.float32), (ops.FORMAT_FP8, torch.bfloat16),
                                              (ops.FORMAT_RAW, None)])
-def test_engine_saves_of_every_path_write_the_oracle_bytes(gpu, fmt, scale_dtype):
+def test_engine_saves_of_every_path_write_the_oracle_bytes(gpu, fmt, scale_dtype, heads, hd):
     # Calls of 1-2 blocks are written to the host slots by a capped grid of save workgroups that stride over
-    # the tiles; 3+ blocks go through staging and a copy. A 48-token block of 3 layers has 144 tiles, which
-    # 128 striding workgroups do not divide evenly.
+    # the tiles; 3+ blocks go through staging and a copy. 48-token blocks of 3 layers do not divide evenly
+    # among the striding workgroups.
     from kvx.engine.cpu_prefix_cache import _CopyEngine
 
     g = torch.Generator(device=gpu).manual_seed(11)
-    pool = (torch.randn((2, 3, 9, 48, 8, 128), generator=g, device=gpu) * 3).to(torch.bfloat16)
+    pool = (torch.randn((2, 3, 9, 48, heads, hd), generator=g, device=gpu) * 3).to(torch.bfloat16)
     layout = ops.pool_layout(pool, scale_dtype)
     engine = _CopyEngine(pool, layout, fmt, split=True)
     try:
