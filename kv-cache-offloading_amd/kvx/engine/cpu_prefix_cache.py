@@ -166,10 +166,12 @@ class _CopyEngine:
 class _CopyBatcher:
     """Hands a cache's saves and restores to its copy engine, in batches inside coalesce().
 
-    One engine call per block costs a cross-stream wait per block: on MI355X
-    one-block restores ran at ~47 GB/s against ~55 GB/s for a batch, and
-    one-block saves beside restores capped both directions together near
-    60 GB/s. Inside coalesce() saves, restores and before_block_reuse waits
+    One engine call per block costs a cross-stream wait per block: on MI355X,
+    with 128 calls queued, one-block restores ran at ~47 GB/s against ~55 GB/s
+    for a batch, and one-block saves beside restores at ~83-86 GB/s against
+    ~94. Batched saves are staged, and slowed concurrent bf16 matmuls by ~10%
+    where one-block saves (written by a kernel) slowed them by 40-60%. Inside
+    coalesce() saves, restores and before_block_reuse waits
     are held back; on exit the saves go first (one call), then the caller's
     stream waits for the blocks passed to before_block_reuse, then the
     restores (one call per run of equal wait flags). Restores with wait=True
