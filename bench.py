@@ -184,6 +184,88 @@ def store_leg(torch, ops, pool, reps=5):
     out["paged_blocks"] = {"tokens": pos, "ms_all_layers": round(1000 * t, 4),
                            "algorithmic_bytes_per_launch": per_launch, "hbm_gbs": round(gbs, 1),
                            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    out["with_concurrent_saves"] = store_beside_saves(torch, ops, pool, key, value, lengths, reps)
+    return out
+
+
+def store_beside_saves(torch, ops, pool, key, value, lengths, reps):
+    """The same batch written while FP8 saves of 64 seeded evicted blocks run on the save stream.
+
+    The batch's slots avoid the evicted blocks (a block being saved is not
+    rewritten). The saves are queued first, one call per block (as the
+    reference's BlockManager issues them) or as one batched call, then the
+    36 store launches on the compute stream. The stores are timed on the
+    compute stream from their first launch; the saves on the save stream from
+    before they were queued; the host time spent queueing the saves is
+    reported beside them.
+    """
+    import numpy as np
+    from types import SimpleNamespace
+
+    from kvx.engine.block_manager import BlockManager
+    from kvx.engine.cpu_prefix_cache import CPUBlockCache
+    from kvx.workloads import block_selection
+
+    _, layers, nb, bs, heads, hd = pool.shape
+    evicted = block_selection(nb, 64, seed=6)
+    excluded = set(evicted)
+    free_slots = np.array([b * bs + i for b in range(nb) if b not in excluded for i in range(bs)])
+    total = int(min(lengths.sum(), free_slots.size))
+    padded = key.shape[0]
+    slots = np.full(padded, -1, dtype=np.int32)
+    slots[:total] = np.random.default_rng(9).permutation(free_slots)[:total]
+    mapping = torch.from_numpy(slots).to(pool.device)
+    manager = BlockManager(nb, bs)
+    keys = []
+    for i, b in enumerate(evicted):
+        tokens = [5000 + i] * bs
+        h = BlockManager.compute_hash(tokens)
+        manager.blocks[b].update(h, tokens)
+        manager.hash_to_block_id[h] = b
+        keys.append(h)
+    runner = SimpleNamespace(world_size=1, block_size=bs, kv_cache=pool)
+    entry = pool[:, :, 0].numel() + pool[:, :, 0].numel() // hd * 4
+    cache = CPUBlockCache(runner, manager, 64 * entry, split_streams=True, fp8=True, scale_dtype=torch.float32,
+                          preallocate=True)
+    compute = torch.cuda.current_stream(pool.device)
+    row = heads * hd * 2
+    per_launch = total * 4 * row + padded * 4
+    out = {"tokens": total, "saved_blocks": 64}
+    try:
+        for mode in ("alone", "per_block_saves", "batched_saves"):
+            store_ms, save_ms, issue_ms = [], [], []
+            for _ in range(reps + 1):
+                cache.clear()
+                torch.cuda.synchronize()
+                start, store_start, store_end, save_end = (torch.cuda.Event(enable_timing=True) for _ in range(4))
+                start.record(compute)
+                t0 = time.perf_counter()
+                if mode == "per_block_saves":
+                    for k in keys:
+                        cache.save_block(k)
+                elif mode == "batched_saves":
+                    with cache.coalesce():
+                        for k in keys:
+                            cache.save_block(k)
+                issue_ms.append(1000 * (time.perf_counter() - t0))
+                store_start.record(compute)
+                for layer in range(layers):
+                    ops.store_kvcache(key, value, pool[0, layer], pool[1, layer], mapping)
+                store_end.record(compute)
+                save_end.record(cache._copy_stream)
+                torch.cuda.synchronize()
+                store_ms.append(store_start.elapsed_time(store_end))
+                save_ms.append(start.elapsed_time(save_end))
+            store_t = sorted(store_ms[1:])[reps // 2] / 1000
+            res = {"store_ms": round(1000 * store_t, 3), "store_hbm_gbs": round(layers * per_launch / store_t / 1e9, 1)}
+            if mode != "alone":
+                save_t = sorted(save_ms[1:])[reps // 2] / 1000
+                res.update({"saves_done_ms": round(1000 * save_t, 3),
+                            "save_link_gbs": round(64 * cache.block_bytes / save_t / 1e9, 2),
+                            "save_issue_host_ms": round(sorted(issue_ms[1:])[reps // 2], 3)})
+            out[mode] = res
+    finally:
+        cache.close()
     return out
 
 
