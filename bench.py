@@ -51,6 +51,8 @@ def parse_args():
     p.add_argument("--skip-host-link", action="store_true")
     p.add_argument("--skip-cpu-baseline", action="store_true")
     p.add_argument("--skip-store", action="store_true", help="skip the store_kvcache leg")
+    p.add_argument("--skip-store-concurrency", action="store_true",
+                   help="skip the store_kvcache leg's run beside concurrent FP8 saves")
     p.add_argument("--skip-hybrid", action="store_true", help="skip the hybrid-admission calibration leg")
     p.add_argument("--skip-agents", action="store_true", help="skip the agent-pressure leg")
     p.add_argument("--skip-handoff", action="store_true", help="skip the KV handoff leg")
@@ -114,7 +116,7 @@ def kernel_leg(torch, ops, pool, sources, dests, scale_dtype, steps, warmup):
                 logical_entry=logical, entry_stride=stride)
 
 
-def store_leg(torch, ops, pool, reps=5):
+def store_leg(torch, ops, pool, reps=5, concurrency=True):
     """store_kvcache over all layers for a ragged batch of 16 sequences (lengths U[1, 8192], seeded).
 
     K is contiguous; V is a strided view of a fused QKV output (row stride
@@ -184,7 +186,8 @@ def store_leg(torch, ops, pool, reps=5):
     out["paged_blocks"] = {"tokens": pos, "ms_all_layers": round(1000 * t, 4),
                            "algorithmic_bytes_per_launch": per_launch, "hbm_gbs": round(gbs, 1),
                            "frac": round(gbs / HBM_PEAK_GBS, 4)}
-    out["with_concurrent_saves"] = store_beside_saves(torch, ops, pool, key, value, lengths, reps)
+    if concurrency:
+        out["with_concurrent_saves"] = store_beside_saves(torch, ops, pool, key, value, lengths, reps)
     return out
 
 
@@ -904,7 +907,7 @@ def main():
     achieved = min(save_gbs, restore_gbs)
     scale_flag = "true" if args.scale == "bf16" else "false"
     kernel_name = (f"fp8_save_kernel<128, 2, 128, {scale_flag}, false>" if dominant == "save"
-                   else f"fp8_restore_kernel<128, 2, 1, {scale_flag}>")
+                   else f"fp8_restore_kernel<128, 2, 64, {scale_flag}>")
     traffic, traffic_source = pmc_traffic(kernel_name)
     log(f"step {ms_per_step:.3f} ms; save {k['save_ms']:.3f} ms ({save_gbs:.0f} GB/s), "
         f"restore {k['restore_ms']:.3f} ms ({restore_gbs:.0f} GB/s)")
@@ -953,7 +956,7 @@ def main():
     }
     if not args.skip_store:
         log("store_kvcache leg")
-        result["store_kvcache"] = store_leg(torch, ops, pool)
+        result["store_kvcache"] = store_leg(torch, ops, pool, concurrency=not args.skip_store_concurrency)
     if args.calibrate_copy:
         raw_layout = ops.pool_layout(pool)
         _, _, raw_stride = ops.entry_layout(raw_layout, ops.FORMAT_RAW)
