@@ -826,3 +826,41 @@ def test_hybrid_requires_automatic_cache(gpu):
     cache = engine.create_cpu_prefix_cache(max_bytes=1 << 20)
     with pytest.raises(ValueError, match="automatic"):
         cache.hybrid = (1.0, 0, 0)
+
+
+# -- bench/test_prefill_scheduling.py --------------------------------------------
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_cpu_restoration_and_prefill_budget_compose(gpu, fp8):
+    """bench/test_prefill_scheduling.py:178-193: a CPU hit admitted under a fixed
+    prefill budget is restored once, then its uncached tail is prefilled in
+    budget-sized chunks. The restored block also holds the saved bytes (BF16
+    byte-exact, FP8 within the reference's per-row bound)."""
+    engine = cached_engine(gpu, [[10], [90], [91], [92], [12]], budget=512, num_blocks=2,
+                           prefill_policy="fixed", prefill_chunk_size=512)
+    manager = engine.scheduler.block_manager
+    engine.add_request([1] * 257, params(max_tokens=1))
+    engine.step_with_events()
+    key = manager.compute_hash([1] * BS)
+    pool = pool_of(engine)
+    before = pool[:, :, manager.hash_to_block_id[key]].clone()
+    size = pool[:, :, 0].numel() * pool.element_size()
+    cache = engine.create_cpu_prefix_cache(size, automatic=True, fp8=fp8)
+    for value, length in ((3, 257), (4, 1)):
+        engine.add_request([value] * length, params(max_tokens=1))
+        engine.step_with_events()
+    assert key not in manager.hash_to_block_id and key in cache
+    engine.scheduler.prefill_chunk_size = 8
+    engine.add_request([1] * 269, params(max_tokens=1))
+    assert engine.step_with_events().num_tokens == 8
+    assert cache.stats["restored_blocks"] == 1
+    torch.cuda.synchronize(pool.device)
+    after = pool[:, :, manager.hash_to_block_id[key]]
+    if fp8:
+        row_amax = before.float().abs().amax(dim=-1, keepdim=True)
+        assert bool(((after.float() - before.float()).abs() <= row_amax / 16).all())
+    else:
+        assert torch.equal(after.view(torch.int16), before.view(torch.int16))
+    assert engine.step_with_events().num_tokens == 5
+    assert engine.is_finished()
+    assert_pool_consistent(manager)
