@@ -118,8 +118,13 @@ def make_pool(device, layers=4, blocks=12, bs=256, heads=8, hd=128, seed=0):
     return (t / chi.add_(1e-3).sqrt() * 0.5).to(torch.bfloat16)
 
 
+# The vector kernels cover head_dim 64, 128 and 256 in tiles of 4-16 rows; the
+# last three geometries leave a ragged last tile in every plane (15, 7 and 6 rows).
 @pytest.mark.parametrize("geometry", [dict(), dict(layers=2, blocks=6, bs=256, heads=1, hd=4),
-                                      dict(layers=3, blocks=7, bs=32, heads=3, hd=96)])
+                                      dict(layers=3, blocks=7, bs=32, heads=3, hd=96),
+                                      dict(layers=2, blocks=6, bs=5, heads=3, hd=128),
+                                      dict(layers=1, blocks=6, bs=7, heads=1, hd=64),
+                                      dict(layers=2, blocks=6, bs=3, heads=2, hd=256)])
 @pytest.mark.parametrize("scale_dtype", [torch.float32, torch.bfloat16])
 def test_fp8_block_save_and_restore_match_the_oracle(gpu, geometry, scale_dtype):
     pool = make_pool(gpu, **geometry)
