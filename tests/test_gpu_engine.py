@@ -10,6 +10,7 @@ instead of torch.Tensor.copy_, since no torch copy is on the path.
 """
 
 from collections import deque
+from contextlib import nullcontext
 
 import pytest
 import torch
@@ -17,10 +18,20 @@ import torch
 from engine_fixtures import (BS, assert_pool_consistent, block_bytes, cached_engine, completed_prefix,
                              finite_prefix, new_cache, overwrite_prefix, params, pool_of, slow_copies,
                              write_scheduled_kv)
-from kvx.engine.cpu_prefix_cache import CPUCacheFullError
+from kvx.engine.cpu_prefix_cache import CPUBlockCache, CPUCacheFullError
 from kvx.engine.sequence import Sequence
 
 pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True, params=["batched", "per_block"])
+def copy_calls(request, monkeypatch):
+    """Every test runs twice: with kvx's block manager handing its loops' copies to the engine in batches
+    (CPUBlockCache.coalesce), and with one engine call per block, the call pattern of the reference's
+    unmodified BlockManager (block_manager.py:97-137, 202-237, 266-336), which has no coalesce()."""
+    if request.param == "per_block":
+        monkeypatch.setattr(CPUBlockCache, "coalesce", lambda self: nullcontext())
+    return request.param
 
 
 # -- bench/test_cpu_prefix_cache.py ---------------------------------------------
