@@ -1,16 +1,23 @@
 """Config 5: agent pressure on the Qwen3-8B pool through the whole engine (store_kvcache, FP8 saves,
 restores and prefetches on split streams under slot reuse), verified block by block."""
 
+from contextlib import nullcontext
+
 import pytest
 import torch
 
+from kvx.engine.cpu_prefix_cache import CPUBlockCache
 from kvx.engine.llm_engine import LLMEngine
 from kvx.workloads import QWEN3_8B, SyntheticKVRunner, run_agent_pressure
 
 pytestmark = pytest.mark.gpu
 
 
-def test_config5_agent_pressure_restores_the_right_bytes(gpu):
+@pytest.mark.parametrize("copy_calls", ["batched", "per_block"])
+def test_config5_agent_pressure_restores_the_right_bytes(gpu, monkeypatch, copy_calls):
+    """per_block: one engine call per save and restore, as the reference's BlockManager issues them."""
+    if copy_calls == "per_block":
+        monkeypatch.setattr(CPUBlockCache, "coalesce", lambda self: nullcontext())
     pool = torch.zeros(QWEN3_8B.shape, dtype=torch.bfloat16, device=gpu)
     engine = LLMEngine(SyntheticKVRunner(pool), max_num_batched_tokens=16384, max_num_seqs=4, eos=-1,
                        kvcache_block_size=256, num_kvcache_blocks=QWEN3_8B.num_blocks)
