@@ -435,22 +435,30 @@ def agent_leg(torch, pool, scale_dtype):
 
     FP8 saves of evicted blocks into an 8 GiB pinned budget, restores and
     prefetch restores of each returning agent's prefix, KV written by
-    store_kvcache. Run once with split save/restore streams and once with one
-    copy stream; link GB/s is entry bytes moved over the run's wall time
+    store_kvcache. Run with split save/restore streams, with one copy stream,
+    and with split streams but one engine call per block (the call pattern of
+    the reference's BlockManager, which has no coalesce()); link GB/s is
+    entry bytes moved over the run's wall time
     (engine, scheduling and the synthetic model included). Each cache pins its
     whole budget when it is created (the reference's preallocate option), so
     neither run's time includes page-locking host memory.
     """
+    from contextlib import nullcontext
+
     from kvx.engine.llm_engine import LLMEngine
     from kvx.workloads import SyntheticKVRunner, run_agent_pressure
 
     out = {"agents": 4, "context_tokens": 32768, "turns": 12, "append_tokens": 2048, "host_budget_bytes": 8 << 30}
-    # The first (untimed, one-turn) run grows torch's allocator for the synthetic model, so neither timed run pays it.
-    for name, split, turns in (("warm-up", True, 1), ("split_streams", True, 12), ("one_copy_stream", False, 12)):
+    # The first (untimed, one-turn) run grows torch's allocator for the synthetic model, so no timed run pays it.
+    runs = (("warm-up", True, 1, True), ("split_streams", True, 12, True), ("one_copy_stream", False, 12, True),
+            ("per_block_calls", True, 12, False))
+    for name, split, turns, batched in runs:
         engine = LLMEngine(SyntheticKVRunner(pool), max_num_batched_tokens=16384, max_num_seqs=4, eos=-1,
                            kvcache_block_size=pool.shape[3], num_kvcache_blocks=pool.shape[2])
-        engine.create_cpu_prefix_cache(8 << 30, automatic=True, prefetch=True, split_streams=split, fp8=True,
-                                       scale_dtype=scale_dtype, preallocate=True)
+        cache = engine.create_cpu_prefix_cache(8 << 30, automatic=True, prefetch=True, split_streams=split,
+                                               fp8=True, scale_dtype=scale_dtype, preallocate=True)
+        if not batched:
+            cache.coalesce = nullcontext  # the block manager then issues one engine call per block
         try:
             r = run_agent_pressure(engine, agents=4, context=32768, turns=turns, append=2048, verify=False)
         finally:
@@ -461,6 +469,7 @@ def agent_leg(torch, pool, scale_dtype):
                      "restored_blocks": r.restored_blocks, "prefetched_blocks": r.prefetched_blocks,
                      "d2h_bytes": r.d2h_bytes, "h2d_bytes": r.h2d_bytes, "link_gbs": round(r.link_gbs, 2)}
     out["split_speedup"] = round(out["one_copy_stream"]["wall_s"] / out["split_streams"]["wall_s"], 3)
+    out["batching_speedup"] = round(out["per_block_calls"]["wall_s"] / out["split_streams"]["wall_s"], 3)
     return out
 
 
