@@ -40,14 +40,19 @@ int check_layout(const kvx_block_layout* layout, int32_t format);
 // Kernel launchers: arguments are validated by the caller.
 // `vector_ok`: the pool base, both strides and every entry allow 16-byte
 // vector access; otherwise the element-granular kernels run.
-// `max_grid` > 0 caps a vector save's workgroups (they then stride over the
-// tiles): for saves written to host memory, which hold their workgroups
-// while the writes cross the host link.
+// `max_grid` > 0 caps a vector kernel's workgroups (they then stride over
+// the tiles): for saves written to and restores read from host memory, which
+// hold their workgroups while the bytes cross the host link.
 hipError_t launch_save(const void* pool, const kvx_block_layout& layout, int32_t format,
                        const BlockBatch& batch, int64_t scale_offset, bool vector_ok, int32_t max_grid,
                        hipStream_t stream);
 hipError_t launch_restore(void* pool, const kvx_block_layout& layout, int32_t format,
-                          const BlockBatch& batch, int64_t scale_offset, bool vector_ok, hipStream_t stream);
+                          const BlockBatch& batch, int64_t scale_offset, bool vector_ok, int32_t max_grid,
+                          hipStream_t stream);
+// True when a restore launched with max_grid > 0 runs the striding kernel,
+// whose reads of host entries are system-scope loads (the element-granular
+// kernels read with plain loads and must not read host memory).
+bool striding_restore_supported(const kvx_block_layout& layout, int32_t format, bool vector_ok);
 // Token gather/scatter between a sequence's blocks and a dense
 // [planes][rows][head_dim] buffer: entries are the dense buffer at
 // block_index * plane_bytes, dense_plane_stride apart per plane, and the

@@ -60,6 +60,23 @@ __device__ __forceinline__ void store16(void* p, uint4 v) {
   else store_nt16(p, v);
 }
 
+// Reads of host memory at system scope (sc0 sc1): never served from a GPU
+// cache line older than the host's or a DMA engine's last write there. Buffer
+// loads through a resource over [base, base + bytes): the compiler tracks them
+// like any other load, and a read past `bytes` returns zeros.
+constexpr int kSystemScope = 1 | 16;  // cache-policy bits sc0 | sc1
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t host_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 load_host16(__amdgpu_buffer_rsrc_t r, int offset) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, kSystemScope);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t load_host32(__amdgpu_buffer_rsrc_t r, int offset) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, offset, 0, kSystemScope);
+}
+
+
 // Workgroups are dispatched round-robin over the chip's 8 XCDs, each with its
 // own L2. Handing each XCD a contiguous range of tiles (instead of every 8th
 // tile) keeps every XCD streaming through one region of memory; on the
@@ -247,6 +264,14 @@ __device__ __forceinline__ float scale_value(const uint8_t* scales, int64_t row,
               : reinterpret_cast<const float*>(scales)[row];
 }
 
+// The same from host memory (`r` covers one plane's scales): the scale's
+// aligned 4-byte word, read at system scope.
+__device__ __forceinline__ float scale_value_host(__amdgpu_buffer_rsrc_t r, int row, bool bf16) {
+  if (!bf16) return __uint_as_float(load_host32(r, row * 4));
+  const uint32_t w = load_host32(r, (row & ~1) * 2);
+  return bf16_bits_to_f32((row & 1) ? w >> 16 : w & 0xFFFFu);
+}
+
 // ---------------------------------------------------------------------------
 // FP8 save / restore, vector path: head_dim = kHd, kVec uint4 (8 bf16) per lane
 // per row, so kHd / (8 * kVec) lanes share one row. A workgroup owns a tile of
@@ -346,14 +371,19 @@ __global__ __launch_bounds__(kBlock) void fp8_save_kernel(const uint16_t* __rest
 // 8-byte code loads cover only half of each 128-byte line per instruction;
 // loading through LDS raised the Qwen3-8B restore from ~6.23 to ~6.49 TB/s
 // (one-wave workgroups; 128 and 256 threads gave ~6.48 and ~6.43).
-template <int kHd, int kVec, int kBlock, bool kScaleBf16>
+// kStride: restores read straight from host slots, by a capped grid whose
+// workgroups stride over the tiles (as the striding save instance).
+template <int kHd, int kVec, int kBlock, bool kScaleBf16, bool kStride>
 __global__ __launch_bounds__(kBlock) void fp8_restore_kernel(uint16_t* __restrict__ pool, PlaneGeom g,
                                                             BlockBatch b) {
   using M = RowMap<kHd, kVec>;
   constexpr int kRows = kBlock / M::kLanes;  // rows per tile
   constexpr int kPieces = kRows * kHd / 16;  // 16-byte pieces of the tile's codes
   __shared__ uint4 codes[kPieces];
-  const TileCoord tc = tile_coord(g, kRows);
+  const int tiles = kStride ? b.n * g.planes * g.chunks : 1;
+  for (int tile = kStride ? (int)blockIdx.x : 0; tile < tiles; tile += kStride ? (int)gridDim.x : 1) {
+  if (kStride) __syncthreads();  // the previous tile's codes have been read back
+  const TileCoord tc = kStride ? tile_coord_at(g, kRows, tile) : tile_coord(g, kRows);
   const int lane = threadIdx.x % M::kLanes;
   const int rsub = threadIdx.x / M::kLanes;
   const int row = tc.row0 + rsub;
@@ -364,16 +394,27 @@ __global__ __launch_bounds__(kBlock) void fp8_restore_kernel(uint16_t* __restric
                           (int64_t)tc.plane * g.plane_rows * (kScaleBf16 ? 2 : 4);
 
   const uint8_t* tile_codes = payload + (int64_t)tc.row0 * kHd;
-  for (int i = threadIdx.x; i < kPieces; i += kBlock)
-    codes[i] = tc.row0 + i * 16 / kHd < g.plane_rows ? load_nt16(tile_codes + i * 16) : make_uint4(0, 0, 0, 0);
-  const float s = row < g.plane_rows ? scale_value(scales, row, kScaleBf16) : 0.0f;
+  float s = 0.0f;
+  if (kStride) {  // entries in host memory
+    const int tile_bytes = (g.plane_rows - tc.row0 < kRows ? g.plane_rows - tc.row0 : kRows) * kHd;
+    const __amdgpu_buffer_rsrc_t rc = host_rsrc(tile_codes, tile_bytes);
+    for (int i = threadIdx.x; i < kPieces; i += kBlock) codes[i] = load_host16(rc, i * 16);
+    if (row < g.plane_rows)
+      s = scale_value_host(host_rsrc(scales, (int64_t)g.plane_rows * (kScaleBf16 ? 2 : 4)), row, kScaleBf16);
+  } else {
+    for (int i = threadIdx.x; i < kPieces; i += kBlock)
+      codes[i] = tc.row0 + i * 16 / kHd < g.plane_rows ? load_nt16(tile_codes + i * 16) : make_uint4(0, 0, 0, 0);
+    if (row < g.plane_rows) s = scale_value(scales, row, kScaleBf16);
+  }
   __syncthreads();
-  if (row >= g.plane_rows) return;
-  const uint2* code_words = reinterpret_cast<const uint2*>(codes);
+  if (row < g.plane_rows) {
+    const uint2* code_words = reinterpret_cast<const uint2*>(codes);
 #pragma unroll
-  for (int v = 0; v < kVec; ++v) {
-    const int col = v * (kHd / kVec) + lane * 8;
-    store_nt16(dst + (int64_t)row * kHd + col, dequantize8(code_words[(rsub * kHd + col) / 8], s));
+    for (int v = 0; v < kVec; ++v) {
+      const int col = v * (kHd / kVec) + lane * 8;
+      store_nt16(dst + (int64_t)row * kHd + col, dequantize8(code_words[(rsub * kHd + col) / 8], s));
+    }
+  }
   }
 }
 
@@ -451,8 +492,8 @@ constexpr int kStrideCopyVecs = 4;
 // Entry e receives plane p of its block at entries[e] + p * entry_plane_stride;
 // every entry copies plane_bytes per plane except the batch's last, which
 // copies last_bytes (a sequence's partial final block in a token gather).
-// kStride: saves to host memory (capped striding grid, system-scope stores),
-// as for fp8_save_kernel.
+// kStride: copies to or from host memory by a capped striding grid, as the
+// FP8 kernels' striding instances; writes to host memory use system-scope stores.
 template <bool kToEntry, bool kStride>
 __global__ __launch_bounds__(kThreads) void raw_copy_kernel(uint8_t* __restrict__ pool, PlaneGeom g,
                                                            BlockBatch b, int64_t plane_bytes,
@@ -477,12 +518,15 @@ __global__ __launch_bounds__(kThreads) void raw_copy_kernel(uint8_t* __restrict_
 #pragma unroll
   for (int k = 0; k < kVecs; ++k) {
     const int64_t off = off0 + ((int64_t)k * kThreads + threadIdx.x) * 16;
-    v[k] = off < valid ? load_nt16(src + off) : make_uint4(0, 0, 0, 0);
+    if (kStride && !kToEntry)  // from host memory; past `valid` the resource reads zeros
+      v[k] = load_host16(host_rsrc(src + off0, valid - off0), (int)(off - off0));
+    else
+      v[k] = off < valid ? load_nt16(src + off) : make_uint4(0, 0, 0, 0);
   }
 #pragma unroll
   for (int k = 0; k < kVecs; ++k) {
     const int64_t off = off0 + ((int64_t)k * kThreads + threadIdx.x) * 16;
-    if (off < valid) store16<kStride>(dst + off, v[k]);
+    if (off < valid) store16<kStride && kToEntry>(dst + off, v[k]);
   }
   }
 }
@@ -658,35 +702,47 @@ template <bool kScaleBf16>
 static hipError_t launch_fp8(bool save, void* pool, const kvx_block_layout& l, const BlockBatch& b,
                              int64_t scale_offset, bool vector_ok, int32_t max_grid, hipStream_t stream) {
   // Workgroup sizes chosen by sweeps on the Qwen3-8B block workload: save
-  // 128 threads (16 rows for hd=128), restore 64 threads (8 rows).
+  // 128 threads (16 rows for hd=128), restore 64 threads (8 rows). A capped
+  // (striding) restore reads host slots and needs more bytes in flight per
+  // workgroup: 256 threads (32 rows).
   constexpr int kSaveBlock = 128;
   constexpr int kRestoreBlock = 64;
-  auto run = [&](auto save_k, auto save_stride_k, auto restore_k, int lanes) -> hipError_t {
-    const int tile = (save ? kSaveBlock : kRestoreBlock) / lanes;
-    PlaneGeom g = make_geom(l, tile, scale_offset);
+  constexpr int kRestoreStrideBlock = 256;
+  auto run = [&](auto save_k, auto save_stride_k, auto restore_k, auto restore_stride_k, int lanes) -> hipError_t {
+    const int block = save ? kSaveBlock : kRestoreBlock;
+    PlaneGeom g = make_geom(l, block / lanes, scale_offset);
     const unsigned grid = (unsigned)(b.n * g.planes * g.chunks);
-    if (save && max_grid > 0 && (unsigned)max_grid < grid)
+    if (save && max_grid > 0 && (unsigned)max_grid < grid) {
       hipLaunchKernelGGL(save_stride_k, dim3((unsigned)max_grid), dim3(kSaveBlock), 0, stream, (const uint16_t*)pool,
                          g, b);
-    else if (save)
+    } else if (save) {
       hipLaunchKernelGGL(save_k, dim3(grid), dim3(kSaveBlock), 0, stream, (const uint16_t*)pool, g, b);
-    else
+    } else if (max_grid > 0) {
+      PlaneGeom gs = make_geom(l, kRestoreStrideBlock / lanes, scale_offset);
+      const unsigned tiles = (unsigned)(b.n * gs.planes * gs.chunks);
+      hipLaunchKernelGGL(restore_stride_k, dim3((unsigned)max_grid < tiles ? (unsigned)max_grid : tiles), dim3(kRestoreStrideBlock), 0,
+                         stream, (uint16_t*)pool, gs, b);
+    } else {
       hipLaunchKernelGGL(restore_k, dim3(grid), dim3(kRestoreBlock), 0, stream, (uint16_t*)pool, g, b);
+    }
     return hipGetLastError();
   };
   switch (vector_ok ? l.head_dim : 0) {
     case 64:
       return run(fp8_save_kernel<64, 1, kSaveBlock, kScaleBf16, false>,
                  fp8_save_kernel<64, 1, kSaveBlock, kScaleBf16, true>,
-                 fp8_restore_kernel<64, 1, kRestoreBlock, kScaleBf16>, RowMap<64, 1>::kLanes);
+                 fp8_restore_kernel<64, 1, kRestoreBlock, kScaleBf16, false>,
+                 fp8_restore_kernel<64, 1, kRestoreStrideBlock, kScaleBf16, true>, RowMap<64, 1>::kLanes);
     case 128:
       return run(fp8_save_kernel<128, 2, kSaveBlock, kScaleBf16, false>,
                  fp8_save_kernel<128, 2, kSaveBlock, kScaleBf16, true>,
-                 fp8_restore_kernel<128, 2, kRestoreBlock, kScaleBf16>, RowMap<128, 2>::kLanes);
+                 fp8_restore_kernel<128, 2, kRestoreBlock, kScaleBf16, false>,
+                 fp8_restore_kernel<128, 2, kRestoreStrideBlock, kScaleBf16, true>, RowMap<128, 2>::kLanes);
     case 256:
       return run(fp8_save_kernel<256, 2, kSaveBlock, kScaleBf16, false>,
                  fp8_save_kernel<256, 2, kSaveBlock, kScaleBf16, true>,
-                 fp8_restore_kernel<256, 2, kRestoreBlock, kScaleBf16>, RowMap<256, 2>::kLanes);
+                 fp8_restore_kernel<256, 2, kRestoreBlock, kScaleBf16, false>,
+                 fp8_restore_kernel<256, 2, kRestoreStrideBlock, kScaleBf16, true>, RowMap<256, 2>::kLanes);
     default: {
       PlaneGeom g = make_geom(l, 0, scale_offset);
       const unsigned grid = generic_grid((int64_t)b.n * l.planes * l.plane_rows);
@@ -716,11 +772,15 @@ static hipError_t launch_raw(bool to_entry, void* pool, const kvx_block_layout& 
       g.chunks = (int32_t)((plane_bytes + tile_bytes - 1) / tile_bytes);
       return g;
     };
-    if (to_entry && max_grid > 0) {
+    if (max_grid > 0) {
       const PlaneGeom g = tiled(kStrideCopyVecs);
       if ((unsigned)max_grid < (unsigned)(b.n * g.planes * g.chunks)) {
-        hipLaunchKernelGGL((raw_copy_kernel<true, true>), dim3((unsigned)max_grid), dim3(kThreads), 0, stream,
-                           (uint8_t*)pool, g, b, plane_bytes, es, entry_plane_stride, last_bytes);
+        if (to_entry)
+          hipLaunchKernelGGL((raw_copy_kernel<true, true>), dim3((unsigned)max_grid), dim3(kThreads), 0, stream,
+                             (uint8_t*)pool, g, b, plane_bytes, es, entry_plane_stride, last_bytes);
+        else
+          hipLaunchKernelGGL((raw_copy_kernel<false, true>), dim3((unsigned)max_grid), dim3(kThreads), 0, stream,
+                             (uint8_t*)pool, g, b, plane_bytes, es, entry_plane_stride, last_bytes);
         return hipGetLastError();
       }
     }
@@ -769,12 +829,19 @@ hipError_t launch_save(const void* pool, const kvx_block_layout& l, int32_t form
              : launch_fp8<false>(true, p, l, b, scale_offset, vector_ok, max_grid, stream);
 }
 
+bool striding_restore_supported(const kvx_block_layout& l, int32_t format, bool vector_ok) {
+  if (!vector_ok) return false;
+  if (format == KVX_FORMAT_RAW) return ((int64_t)l.plane_rows * l.head_dim * l.elem_bytes) % 16 == 0;
+  return l.head_dim == 64 || l.head_dim == 128 || l.head_dim == 256;  // launch_fp8's vector kernels
+}
+
 hipError_t launch_restore(void* pool, const kvx_block_layout& l, int32_t format, const BlockBatch& b,
-                          int64_t scale_offset, bool vector_ok, hipStream_t stream) {
+                          int64_t scale_offset, bool vector_ok, int32_t max_grid, hipStream_t stream) {
   if (b.n <= 0) return hipSuccess;
-  if (format == KVX_FORMAT_RAW) return launch_raw(false, pool, l, b, vector_ok, -1, -1, 0, stream);
-  return l.scale_dtype == KVX_SCALE_BF16 ? launch_fp8<true>(false, pool, l, b, scale_offset, vector_ok, 0, stream)
-                                         : launch_fp8<false>(false, pool, l, b, scale_offset, vector_ok, 0, stream);
+  if (format == KVX_FORMAT_RAW) return launch_raw(false, pool, l, b, vector_ok, -1, -1, max_grid, stream);
+  return l.scale_dtype == KVX_SCALE_BF16
+             ? launch_fp8<true>(false, pool, l, b, scale_offset, vector_ok, max_grid, stream)
+             : launch_fp8<false>(false, pool, l, b, scale_offset, vector_ok, max_grid, stream);
 }
 
 hipError_t launch_store_kvcache(const void* key, int64_t key_stride, const void* value, int64_t value_stride,

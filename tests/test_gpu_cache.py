@@ -463,6 +463,52 @@ def test_engine_saves_of_every_path_write_the_oracle_bytes(gpu, fmt, scale_dtype
         engine.close()
 
 
+@pytest.mark.parametrize("heads,hd", [(8, 128), (4, 64), (2, 256)])
+@pytest.mark.parametrize("fmt,scale_dtype", [(ops.FORMAT_FP8, torch.float32), (ops.FORMAT_FP8, torch.bfloat16),
+                                             (ops.FORMAT_RAW, None)])
+def test_engine_restores_of_every_path_write_the_oracle_bytes(gpu, fmt, scale_dtype, heads, hd):
+    # With no save in flight, waited restores of 1-2 blocks are read from the host slots by a capped grid of
+    # restore workgroups; 3+ blocks, and restores nobody waits for, go through staging and a copy. 50-token
+    # blocks leave a ragged last tile in every plane.
+    from kvx.engine.cpu_prefix_cache import _CopyEngine
+
+    g = torch.Generator(device=gpu).manual_seed(12)
+    pool = (torch.randn((2, 3, 9, 50, heads, hd), generator=g, device=gpu) * 3).to(torch.bfloat16)
+    layout = ops.pool_layout(pool, scale_dtype)
+    engine = _CopyEngine(pool, layout, fmt, split=True)
+    try:
+        stride = engine.entry_stride
+        slab = torch.full((8 * stride,), 0xA5, dtype=torch.uint8, pin_memory=True)
+        staging = [torch.empty(4 * stride, dtype=torch.uint8, device=gpu) for _ in range(2)]
+        engine.add_slab(slab, 8)
+        engine.set_staging(*staging, 4)
+        compute = torch.cuda.current_stream(gpu).cuda_stream
+        sources = [7, 2, 5, 0, 8, 3, 6, 1]  # slot i holds block sources[i]
+        engine.save(sources, list(range(8)), compute)
+        engine.synchronize()
+        host_pool = bf16_bits(pool)
+        fp32 = scale_dtype == torch.float32
+        calls = [([0], [4], True), ([1, 2], [7, 0], True), ([3, 4, 5], [1, 2, 3], True), ([6], [5], False),
+                 ([7], [6], True)]
+        for slots, blocks, wait in calls:
+            engine.restore(slots, blocks, wait, compute)
+        engine.synchronize()
+        after = bf16_bits(pool)
+        for slots, blocks, _ in calls:
+            for slot, d in zip(slots, blocks):
+                b = sources[slot]
+                if fmt == ops.FORMAT_RAW:
+                    expect = host_pool[:, :, b]
+                else:
+                    codes, scales = oracle.save_block_fp8(host_pool, b, fp32)
+                    expect = oracle.dequantize(codes, scales, fp32)
+                assert np.array_equal(after[:, :, d], expect), (slot, b, d)
+        assert np.array_equal(after[:, :, 8], host_pool[:, :, 8])  # never a destination
+        assert engine.counters()["restored_blocks"] == 8
+    finally:
+        engine.close()
+
+
 def test_a_failed_batch_withdraws_the_metadata_it_published(gpu, monkeypatch):
     pool = make_pool(gpu, 6)
     manager = BlockManager(6, BS)
