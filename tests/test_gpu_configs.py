@@ -1,6 +1,8 @@
 """Parity at the benchmark configurations' full sizes (Qwen3-0.6B / Qwen3-8B KV geometry).
 
 Config 1: FP8 save of 16 seeded blocks of a [2,28,512,256,8,128] pool, restore into 16 other seeded blocks.
+Config 2: FP8 save (fp32 scales) of 128 seeded blocks of the Student-t Qwen3-8B pool [2,36,320,256,8,128] to
+          pinned host slots through the copy engine, restore into 128 other seeded blocks.
 Config 3: BF16 byte-exact save of 200 scattered Qwen3-8B blocks to pinned host slots and restore into a seeded
           permutation of free blocks that overlaps the sources; hybrid admission of a 32,768-token prefix that
           restores only its tail.
@@ -82,6 +84,55 @@ def test_config1_fp8_round_trip_of_16_blocks(gpu):
         assert np.array_equal(staged[i, :codes.size], codes.ravel())
         assert np.array_equal(staged[i, offset:offset + rows * 4], scales.view(np.uint8).ravel())
         assert np.array_equal(bf16_bits(pool[:, :, dests[i]]), oracle.dequantize(codes, scales, True))
+
+
+def test_config2_fp8_128_blocks_through_pinned_slots(gpu):
+    from kvx.engine.cpu_prefix_cache import _CopyEngine
+
+    pool = torch.empty(QWEN3_8B.shape, dtype=torch.bfloat16, device=gpu)
+    fill_student_t(pool, seed=0)  # bf16(0.5 t4), 4 seeded x20 outlier channels per (kv, layer, head)
+    order = block_selection(QWEN3_8B.num_blocks, 256, seed=1)
+    sources, dests = order[:128], order[128:]
+    layout = ops.pool_layout(pool, torch.float32)
+    engine = _CopyEngine(pool, layout, ops.FORMAT_FP8, split=True)
+    try:
+        stride, offset = engine.entry_stride, engine.scale_offset
+        slab = torch.full((128 * stride,), 0xAB, dtype=torch.uint8, pin_memory=True)
+        staging = [torch.empty(32 * stride, dtype=torch.uint8, device=gpu) for _ in range(2)]
+        engine.add_slab(slab, 128)
+        engine.set_staging(*staging, 32)
+        compute = torch.cuda.current_stream(gpu).cuda_stream
+        source_copy = pool[:, :, sources].clone()
+        others = sorted(set(range(QWEN3_8B.num_blocks)) - set(dests))
+        canary = pool[:, :, others].clone()
+        engine.save(sources, list(range(128)), compute)
+        engine.restore(list(range(128)), dests, False, compute)
+        engine.before_block_use(dests[0], compute)  # (all 128 share one restore event)
+        engine.synchronize()
+        torch.cuda.synchronize()
+        rows = layout.planes * layout.plane_rows
+        shape = source_copy[:, :, 0].shape
+        entries = slab.view(128, stride)
+        for i in range(128):
+            # Size-independent checks on the device for every block: the restore is the reference's dequantize of
+            # the host entry (fp32 code x fp32 scale, one rounding to bf16), within the reference's bound.
+            entry = entries[i].to(gpu)
+            codes = entry[:rows * layout.head_dim].view(torch.float8_e4m3fn).view(shape)
+            scales = entry[offset:offset + rows * 4].view(torch.float32).view(*shape[:-1], 1)
+            expect = (codes.float() * scales).to(torch.bfloat16)
+            got = pool[:, :, dests[i]]
+            assert same_bytes(got, expect), f"block {sources[i]} -> {dests[i]}"
+            src = source_copy[:, :, i].float()
+            assert torch.all((got.float() - src).abs() <= src.abs().amax(-1, keepdim=True) / 16)
+        host = entries.numpy()
+        for i in (0, 63, 127):  # bit-exact against the oracle on a sample
+            codes, scales = oracle.quantize(bf16_bits(source_copy[:, :, i]), True)
+            assert np.array_equal(host[i, :codes.size], codes.ravel()), f"payload of block {sources[i]}"
+            assert np.array_equal(host[i, offset:offset + rows * 4], scales.view(np.uint8).ravel())
+            assert np.array_equal(bf16_bits(pool[:, :, dests[i]]), oracle.dequantize(codes, scales, True))
+        assert same_bytes(pool[:, :, others], canary)  # no block outside the destinations was written
+    finally:
+        engine.close()
 
 
 def test_config3_bf16_200_blocks_into_permuted_free_blocks(gpu):
