@@ -76,7 +76,6 @@ __device__ __forceinline__ uint32_t load_host32(__amdgpu_buffer_rsrc_t r, int of
   return __builtin_amdgcn_raw_buffer_load_b32(r, offset, 0, kSystemScope);
 }
 
-
 // Workgroups are dispatched round-robin over the chip's 8 XCDs, each with its
 // own L2. Handing each XCD a contiguous range of tiles (instead of every 8th
 // tile) keeps every XCD streaming through one region of memory; on the
@@ -483,9 +482,9 @@ __global__ __launch_bounds__(kThreads) void fp8_restore_generic(uint16_t* __rest
 // uint4 per thread per tile. Device-side copies use 8 KiB tiles with
 // nontemporal loads and stores: on 128 Qwen3-8B blocks, gather 5.93 -> 6.23
 // and scatter 5.83 -> 6.22 TB/s against 16 KiB tiles with plain loads
-// (4 KiB tiles from 128 threads: 6.27 gather). Striding saves to host memory
-// keep 16 KiB tiles: their few workgroups need the larger tiles in flight to
-// keep the host link busy.
+// (4 KiB tiles from 128 threads: 6.27 gather). Striding copies to or from
+// host memory keep 16 KiB tiles: their few workgroups need the larger tiles
+// in flight to keep the host link busy.
 constexpr int kCopyVecs = 2;
 constexpr int kStrideCopyVecs = 4;
 
