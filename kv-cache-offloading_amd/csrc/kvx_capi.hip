@@ -294,9 +294,14 @@ struct kvx_cache {
     return hip_status(hipStreamWaitEvent(s, e->ev, 0), "hipStreamWaitEvent");
   }
 
-  // `dst` waits for all work queued so far on `src`.
+  // `dst` waits for all work queued so far on `src`. An idle `src` needs no
+  // wait: between engine steps the caller's stream has usually drained (the
+  // step's sampled tokens were read back), and skipping the marker event and
+  // cross-stream wait there raised 128 queued one-block FP8 restores from
+  // 46.5-48.1 to 52.8 GB/s and one-block saves beside restores from 85-86 to
+  // 87-94 GB/s on MI355X.
   int wait_stream(hipStream_t dst, hipStream_t src) {
-    if (dst == src) return KVX_OK;
+    if (dst == src || hipStreamQuery(src) == hipSuccess) return KVX_OK;
     int rc = hip_status(hipEventRecord(marker, src), "hipEventRecord");
     if (rc) return rc;
     ++waits;
