@@ -182,8 +182,9 @@ int kvx_cache_streams(kvx_cache* cache, void** save_stream, void** restore_strea
  * on compute_stream, for the last restore that read each slot and for any
  * background restore still writing each block; a "save done" event then
  * marks each block (for before_block_reuse) and each slot (for a later
- * restore of it). Calls of one or two blocks have the save kernel write
- * the slots itself; larger ones go through device staging and a copy.
+ * restore of it). Calls of one or two blocks issued while compute_stream
+ * still has work queued have the save kernel write the slots itself; other
+ * calls go through device staging and a copy.
  * Slabs must be pinned, device-accessible host memory (hipHostMalloc).
  * A slot may appear only once per call (KVX_E_INVALID).
  */

@@ -300,8 +300,11 @@ struct kvx_cache {
   // cross-stream wait there raised 128 queued one-block FP8 restores from
   // 46.5-48.1 to 52.8 GB/s and one-block saves beside restores from 85-86 to
   // 87-94 GB/s on MI355X.
-  int wait_stream(hipStream_t dst, hipStream_t src) {
-    if (dst == src || hipStreamQuery(src) == hipSuccess) return KVX_OK;
+  // *needed (optional) tells whether a wait was queued.
+  int wait_stream(hipStream_t dst, hipStream_t src, bool* needed = nullptr) {
+    const bool wait = dst != src && hipStreamQuery(src) != hipSuccess;
+    if (needed) *needed = wait;
+    if (!wait) return KVX_OK;
     int rc = hip_status(hipEventRecord(marker, src), "hipEventRecord");
     if (rc) return rc;
     ++waits;
@@ -324,18 +327,24 @@ struct kvx_cache {
     return KVX_OK;
   }
 
-  // Saves of one or two blocks have the save kernel write the pinned slots
-  // itself; larger calls gather into staging and copy to the host. Measured
-  // on MI355X with Qwen3-8B FP8 blocks and a restore stream running beside
-  // the save stream (save alone / both directions, GB/s):
-  //  - staged, 1-2 blocks per call: the D2H copy of the entries, queued behind
-  //    the save kernel whose stream waited for a still-busy compute stream,
-  //    started ~0.65 ms late: 29.6 / 32 (one block), 53 / 42.5 (two blocks;
-  //    92.6 when the compute stream was idle). Three or more blocks never
-  //    showed it: 53.8-54.9 / 92.7-94.5;
+  // Saves of one or two blocks issued while the caller's stream still has
+  // work queued have the save kernel write the pinned slots itself; other
+  // saves gather into staging and copy to the host. Measured on MI355X with
+  // Qwen3-8B FP8 blocks and a restore stream running beside the save stream
+  // (save alone / both directions, GB/s):
+  //  - staged, 1-2 blocks per call behind a busy caller stream: the D2H copy
+  //    of the entries, queued behind the save kernel whose stream waited for
+  //    the caller's, started ~0.65 ms late: 29.6 / 32 (one block), 53 / 42.5
+  //    (two blocks). Three or more blocks never showed it: 53.8-54.9 /
+  //    92.7-94.5. With the caller's stream idle (no wait) one-block saves run
+  //    at 51.5 / 90-92;
   //  - written by the kernel (direct_save_grid workgroups, system-scope
-  //    stores): 48.7-48.8 / 93.0 for one block, 49.5 / 93.5-93.8 for two.
-  static bool direct_save(int32_t n) { return n <= 2; }
+  //    stores): 48.7-49.3 / 93-93.5 for one block, 49.5 / 93.5-93.8 for two.
+  // Kernel-written saves hold CUs for the whole transfer: 64 one-block FP8
+  // saves queued before 200 bf16 4096^2 matmuls left the matmuls 29.5 ms
+  // against 23.8 ms beside staged saves (19.8 ms alone), so they are used
+  // only where the staged copy would start late.
+  static bool direct_save(int32_t n, bool caller_busy) { return n <= 2 && caller_busy; }
 
   // Workgroups of a save that writes host slots directly. The launch lasts as
   // long as its writes take to cross the host link (~0.4 ms per Qwen3-8B FP8
@@ -604,7 +613,8 @@ int kvx_cache_save(kvx_cache* c, const int32_t* ids, const int32_t* slots, int32
   if (rc) return rc;
   hipStream_t s = c->save_stream;
   // Start after the kernels that wrote these blocks (cpu_prefix_cache.py:310-311).
-  rc = c->wait_stream(s, (hipStream_t)compute_stream);
+  bool caller_busy = false;
+  rc = c->wait_stream(s, (hipStream_t)compute_stream, &caller_busy);
   if (rc) return rc;
   // With split streams, after the last restore that read each target slot (:312-314).
   if (c->split && !(c->debug & KVX_DEBUG_SKIP_SLOT_READ_WAIT)) {
@@ -627,7 +637,7 @@ int kvx_cache_save(kvx_cache* c, const int32_t* ids, const int32_t* slots, int32
       }
     }
   }
-  if (kvx_cache::direct_save(n)) {
+  if (kvx_cache::direct_save(n, caller_busy)) {
     rc = c->launch(true, ids, nullptr, slots, n, s);
     if (rc) return rc;
   } else {

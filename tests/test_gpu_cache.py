@@ -421,13 +421,14 @@ def test_engine_rejects_two_copies_into_one_destination(gpu):
     cache.close()
 
 
+@pytest.mark.parametrize("caller_busy", [False, True])
 @pytest.mark.parametrize("heads,hd", [(8, 128), (4, 64), (2, 256)])
 @pytest.mark.parametrize("fmt,scale_dtype", [(ops.FORMAT_FP8, torch.float32), (ops.FORMAT_FP8, torch.bfloat16),
                                              (ops.FORMAT_RAW, None)])
-def test_engine_saves_of_every_path_write_the_oracle_bytes(gpu, fmt, scale_dtype, heads, hd):
-    # Calls of 1-2 blocks are written to the host slots by a capped grid of save workgroups that stride over
-    # the tiles; 3+ blocks go through staging and a copy. 48-token blocks of 3 layers do not divide evenly
-    # among the striding workgroups.
+def test_engine_saves_of_every_path_write_the_oracle_bytes(gpu, fmt, scale_dtype, heads, hd, caller_busy):
+    # Calls of 1-2 blocks issued while the caller's stream is busy are written to the host slots by a capped grid
+    # of save workgroups that stride over the tiles; other calls go through staging and a copy. 48-token blocks
+    # of 3 layers do not divide evenly among the striding workgroups.
     from kvx.engine.cpu_prefix_cache import _CopyEngine
 
     g = torch.Generator(device=gpu).manual_seed(11)
@@ -443,6 +444,8 @@ def test_engine_saves_of_every_path_write_the_oracle_bytes(gpu, fmt, scale_dtype
         compute = torch.cuda.current_stream(gpu).cuda_stream
         calls = [([7], [0]), ([2, 5], [1, 2]), ([0, 8, 3], [3, 4, 5]), ([1, 6], [7, 6])]
         for blocks, slots in calls:
+            if caller_busy:
+                ops.sleep(2000, device=gpu)  # on the caller's (current) stream
             engine.save(blocks, slots, compute)
         engine.synchronize()
         host_pool = bf16_bits(pool)
