@@ -916,7 +916,7 @@ def main():
     achieved = min(save_gbs, restore_gbs)
     scale_flag = "true" if args.scale == "bf16" else "false"
     kernel_name = (f"fp8_save_kernel<128, 2, 128, {scale_flag}, false>" if dominant == "save"
-                   else f"fp8_restore_kernel<128, 2, 64, {scale_flag}>")
+                   else f"fp8_restore_kernel<128, 2, 64, {scale_flag}, false>")
     traffic, traffic_source = pmc_traffic(kernel_name)
     log(f"step {ms_per_step:.3f} ms; save {k['save_ms']:.3f} ms ({save_gbs:.0f} GB/s), "
         f"restore {k['restore_ms']:.3f} ms ({restore_gbs:.0f} GB/s)")
