@@ -14,6 +14,7 @@ from dataclasses import dataclass, fields
 import torch
 
 from kvx.engine import kv_handoff
+from kvx.engine.handoff_timing import PhaseTimer
 from kvx.engine.cpu_prefix_cache import CPUBlockCache
 from kvx.engine.scheduler import Scheduler, validate_scheduling_options
 from kvx.engine.sequence import SamplingParams, Sequence
@@ -132,9 +133,13 @@ class LLMEngine:
         seq = next((seq for seq in self.scheduler.running if seq.seq_id == seq_id), None)
         if seq is None:
             raise ValueError(f"request {seq_id} is not running at a handoff boundary")
-        snapshot = kv_handoff.export_kv(self.model_runner, seq)
-        self._detached_requests[seq_id] = seq
-        self.scheduler.running.remove(seq)
+        timer = PhaseTimer("detach_request", seq_id=seq_id)
+        with timer.phase("export"):
+            snapshot = kv_handoff.export_kv(self.model_runner, seq)
+        with timer.phase("unschedule"):
+            self._detached_requests[seq_id] = seq
+            self.scheduler.running.remove(seq)
+        timer.finish()
         return snapshot
 
     def release_detached_request(self, seq_id: int):
@@ -151,17 +156,23 @@ class LLMEngine:
     def resume_request(self, snapshot: kv_handoff.KVSnapshot) -> int:
         """Import a snapshot as a running request; admit it only once its KV is on the device."""
         manager = self.scheduler.block_manager
+        timer = PhaseTimer("resume_request")
         seq = None
         try:
-            seq = kv_handoff.import_kv(self.model_runner, manager, snapshot)
-            device = self.model_runner.kv_cache.device
-            if device.type == "cuda":
-                torch.cuda.synchronize(device)
-            self.scheduler.running.append(seq)
-        except Exception:
+            with timer.phase("import"):
+                seq = kv_handoff.import_kv(self.model_runner, manager, snapshot)
+            with timer.phase("cuda_sync"):
+                device = self.model_runner.kv_cache.device
+                if device.type == "cuda":
+                    torch.cuda.synchronize(device)
+            with timer.phase("admit"):
+                self.scheduler.running.append(seq)
+        except Exception as error:
+            timer.abort(error)
             if seq is not None:
                 manager.deallocate(seq)
             raise
+        timer.finish(seq_id=seq.seq_id)
         return seq.seq_id
 
     def step(self):

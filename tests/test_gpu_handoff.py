@@ -263,3 +263,40 @@ def test_exit_releases_detached_source_blocks(gpu):
     source.exit()
     assert not source._detached_requests and not manager.used_block_ids
     assert source.model_runner.calls[-1] == "exit"
+
+
+def test_detach_and_resume_emit_phase_records(gpu, caplog):
+    """bench/test_handoff_timing.py:118-151."""
+    import json
+    import logging
+
+    import kvx.engine.handoff_timing as timing
+
+    caplog.set_level(logging.DEBUG, logger="nanovllm.kv_handoff")
+    timing.enable(True)
+    try:
+        source, source_id = prefilled_engine(gpu, length=5)
+        snapshot = source.detach_request(source_id)
+        records = [json.loads(r.message) for r in caplog.records]
+        assert [r["op"] for r in records] == ["export_kv", "detach_request"]
+        export, detach = records
+        assert set(export["phases_ms"]) == {"gather_blocks", "pack", "copy_to_host"}
+        assert set(detach["phases_ms"]) == {"export", "unschedule"}
+        assert export["num_tokens"] == 5
+        assert snapshot.payload_bytes == export["payload_bytes"] > 0
+
+        caplog.records.clear()
+        destination = cached_engine(gpu, [[11], [12]])
+        destination.model_runner.kv_cache.fill_(-1)
+        destination.resume_request(snapshot)
+        records = [json.loads(r.message) for r in caplog.records]
+        assert [r["op"] for r in records] == ["import_kv", "resume_request"]
+        imported, resume = records
+        assert set(imported["phases_ms"]) == {"validate", "rebuild_sequence", "allocate_blocks", "copy_to_device",
+                                              "scatter_blocks", "publish_cache"}
+        assert set(resume["phases_ms"]) == {"import", "cuda_sync", "admit"}
+        assert resume["seq_id"] == destination.scheduler.running[0].seq_id
+        assert imported["total_ms"] <= resume["phases_ms"]["import"] + 1e-3  # nested: import inside resume's phase
+        assert kv_handoff.verify_imported_kv(destination.model_runner, destination.scheduler.running[0], snapshot)
+    finally:
+        timing.enable(False)
