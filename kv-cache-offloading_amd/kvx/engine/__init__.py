@@ -1,1 +1,2 @@
-"""Engine-side callers of the copy path: block manager, CPU block cache, scheduler."""
+"""Engine-side callers of the copy path: block manager, CPU block cache, scheduler, model-free engine,
+KV handoff and its phase timing."""
