@@ -373,3 +373,41 @@ def test_empty_and_all_padding_inputs_are_no_ops(gpu):
     ops.scatter_tokens(pool, [], 0, dense)
     torch.cuda.synchronize()
     assert torch.equal(pool.view(torch.int16), before.view(torch.int16))
+
+
+def test_calls_longer_than_one_launch_cover_every_block(gpu):
+    # A launch covers at most 128 blocks and longer calls are split: 150 blocks
+    # (a ragged second launch of 22) through the FP8 codec and the token copies.
+    pool = make_pool(gpu, layers=2, blocks=320, bs=4, heads=2, hd=128, seed=3)
+    nb, bs = pool.shape[2], pool.shape[3]
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(11)).tolist()
+    sources, dests = perm[:150], perm[150:300]
+    src_bits = bf16_bits(pool)
+    untouched = [b for b in range(nb) if b not in set(dests)]
+    for scale_dtype in (torch.float32, torch.bfloat16):
+        fp32 = scale_dtype == torch.float32
+        layout = ops.pool_layout(pool, scale_dtype)
+        _, _, stride = ops.entry_layout(layout, ops.FORMAT_FP8)
+        staging = torch.full((len(sources) * stride,), 0xAB, dtype=torch.uint8, device=gpu)
+        entries = [staging.data_ptr() + i * stride for i in range(len(sources))]
+        target = pool.clone()
+        ops.save_blocks(pool, sources, entries, ops.FORMAT_FP8, scale_dtype)
+        ops.restore_blocks(target, dests, entries, ops.FORMAT_FP8, scale_dtype)
+        after = bf16_bits(target)
+        for b, d in zip(sources, dests):
+            codes, scales = oracle.save_block_fp8(src_bits, b, fp32)
+            assert np.array_equal(after[:, :, d], oracle.dequantize(codes, scales, fp32)), (scale_dtype, b, d)
+        assert np.array_equal(after[:, :, untouched], src_bits[:, :, untouched])
+    # Token copies: 597 tokens span 150 blocks, the last holding one token.
+    tokens = len(sources) * bs - 3
+    dense = torch.empty((2, pool.shape[1], tokens, *pool.shape[-2:]), dtype=pool.dtype, device=gpu)
+    ops.gather_tokens(pool, sources, tokens, dense)
+    expect = src_bits[:, :, sources].reshape(2, pool.shape[1], len(sources) * bs, *pool.shape[-2:])[:, :, :tokens]
+    assert np.array_equal(bf16_bits(dense), expect)
+    target = pool.clone()
+    ops.scatter_tokens(target, dests, tokens, dense)
+    after = bf16_bits(target)
+    written = after[:, :, dests].reshape(2, pool.shape[1], len(dests) * bs, *pool.shape[-2:])
+    assert np.array_equal(written[:, :, :tokens], expect)
+    assert np.array_equal(after[:, :, dests[-1], 1:], src_bits[:, :, dests[-1], 1:])
+    assert np.array_equal(after[:, :, untouched], src_bits[:, :, untouched])
