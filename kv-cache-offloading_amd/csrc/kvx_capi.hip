@@ -289,7 +289,17 @@ struct kvx_cache {
     if (e->refs == 0) free_events.push_back(e);
   }
 
+  // `s` waits for `e`. An event that has already completed orders nothing
+  // queued from now on, so it costs no wait: a one-block restore used to
+  // queue one on its slot's long-finished save.
   int wait_event(hipStream_t s, Event* e) {
+    const hipError_t q = hipEventQuery(e->ev);
+    if (q == hipSuccess) return KVX_OK;
+    if (q != hipErrorNotReady) return hip_status(q, "hipEventQuery");
+    return queue_wait(s, e);
+  }
+
+  int queue_wait(hipStream_t s, Event* e) {
     ++waits;
     return hip_status(hipStreamWaitEvent(s, e->ev, 0), "hipStreamWaitEvent");
   }
@@ -709,7 +719,7 @@ int kvx_cache_restore(kvx_cache* c, const int32_t* slots, const int32_t* ids, in
   Event* done = nullptr;
   rc = c->new_event(&done);
   if (!rc) rc = hip_status(hipEventRecord(done->ev, s), "hipEventRecord");
-  if (!rc && wait) rc = c->wait_event(compute, done);
+  if (!rc && wait) rc = c->queue_wait(compute, done);
   if (rc) {
     if (done) c->release_if_unused(done);
     return rc;
