@@ -86,14 +86,17 @@ def test_config1_fp8_round_trip_of_16_blocks(gpu):
         assert np.array_equal(bf16_bits(pool[:, :, dests[i]]), oracle.dequantize(codes, scales, True))
 
 
-def test_config2_fp8_128_blocks_through_pinned_slots(gpu):
+@pytest.mark.parametrize("scale_dtype", [torch.float32, torch.bfloat16])
+def test_config2_fp8_128_blocks_through_pinned_slots(gpu, scale_dtype):
     from kvx.engine.cpu_prefix_cache import _CopyEngine
 
     pool = torch.empty(QWEN3_8B.shape, dtype=torch.bfloat16, device=gpu)
     fill_student_t(pool, seed=0)  # bf16(0.5 t4), 4 seeded x20 outlier channels per (kv, layer, head)
     order = block_selection(QWEN3_8B.num_blocks, 256, seed=1)
     sources, dests = order[:128], order[128:]
-    layout = ops.pool_layout(pool, torch.float32)
+    fp32 = scale_dtype == torch.float32
+    sbytes = 4 if fp32 else 2
+    layout = ops.pool_layout(pool, scale_dtype)
     engine = _CopyEngine(pool, layout, ops.FORMAT_FP8, split=True)
     try:
         stride, offset = engine.entry_stride, engine.scale_offset
@@ -115,21 +118,22 @@ def test_config2_fp8_128_blocks_through_pinned_slots(gpu):
         entries = slab.view(128, stride)
         for i in range(128):
             # Size-independent checks on the device for every block: the restore is the reference's dequantize of
-            # the host entry (fp32 code x fp32 scale, one rounding to bf16), within the reference's bound.
+            # the host entry (fp32 code x scale, one rounding to bf16; exact product for bf16 scales), within the
+            # reference's bound.
             entry = entries[i].to(gpu)
             codes = entry[:rows * layout.head_dim].view(torch.float8_e4m3fn).view(shape)
-            scales = entry[offset:offset + rows * 4].view(torch.float32).view(*shape[:-1], 1)
-            expect = (codes.float() * scales).to(torch.bfloat16)
+            scales = entry[offset:offset + rows * sbytes].view(scale_dtype).view(*shape[:-1], 1)
+            expect = (codes.float() * scales.float()).to(torch.bfloat16)
             got = pool[:, :, dests[i]]
             assert same_bytes(got, expect), f"block {sources[i]} -> {dests[i]}"
             src = source_copy[:, :, i].float()
             assert torch.all((got.float() - src).abs() <= src.abs().amax(-1, keepdim=True) / 16)
         host = entries.numpy()
         for i in (0, 63, 127):  # bit-exact against the oracle on a sample
-            codes, scales = oracle.quantize(bf16_bits(source_copy[:, :, i]), True)
+            codes, scales = oracle.quantize(bf16_bits(source_copy[:, :, i]), fp32)
             assert np.array_equal(host[i, :codes.size], codes.ravel()), f"payload of block {sources[i]}"
-            assert np.array_equal(host[i, offset:offset + rows * 4], scales.view(np.uint8).ravel())
-            assert np.array_equal(bf16_bits(pool[:, :, dests[i]]), oracle.dequantize(codes, scales, True))
+            assert np.array_equal(host[i, offset:offset + rows * sbytes], scales.view(np.uint8).ravel())
+            assert np.array_equal(bf16_bits(pool[:, :, dests[i]]), oracle.dequantize(codes, scales, fp32))
         assert same_bytes(pool[:, :, others], canary)  # no block outside the destinations was written
     finally:
         engine.close()
