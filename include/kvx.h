@@ -190,6 +190,27 @@ int kvx_cache_streams(kvx_cache* cache, void** save_stream, void** restore_strea
  */
 int kvx_cache_save(kvx_cache* cache, const int32_t* block_ids_host, const int32_t* slots_host,
                    int32_t n, void* compute_stream);
+
+/* Bytes of the static device staging behind kvx_cache_save_noalloc, one array per device. */
+#define KVX_NOALLOC_SCRATCH_BYTES (64LL << 20)
+
+/*
+ * kvx_cache_save without attached staging and without allocation. It has no
+ * counterpart in the reference: it is for callers that cannot allocate
+ * (serving loops and harnesses that forbid hipMalloc, or processes whose
+ * device memory all belongs to the KV pool). Ordering, results and errors
+ * are those of kvx_cache_save, except that entries are staged in a static
+ * array of KVX_NOALLOC_SCRATCH_BYTES that the library holds on each device
+ * until the process ends, and that the call creates no events and allocates
+ * no host or device memory. n may not exceed the entries that array holds,
+ * min(128, KVX_NOALLOC_SCRATCH_BYTES / entry_stride) (three Qwen3-8B FP8
+ * entries); a larger n fails with KVX_E_RANGE before any work is queued.
+ * Every such call on one device shares its array: calls queued on one save
+ * stream run in order, but calls of different caches (different save
+ * streams) that overlap in time race and produce wrong bytes.
+ */
+int kvx_cache_save_noalloc(kvx_cache* cache, const int32_t* block_ids_host, const int32_t* slots_host,
+                           int32_t n, void* compute_stream);
 /*
  * Restores host slots slots_host[i] into pool blocks block_ids_host[i]
  * (_copy_entry, :370-398). The restore stream waits for compute_stream, for

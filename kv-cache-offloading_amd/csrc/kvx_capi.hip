@@ -5,6 +5,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <new>
 #include <utility>
 #include <vector>
@@ -75,9 +76,16 @@ static void entry_sizes(const kvx_block_layout& l, int32_t format, int64_t* logi
 }
 
 // True if two of the n values are equal: two copies into one destination
-// in one call would race, so calls reject it.
+// in one call would race, so calls reject it. Lists of up to kMaxBatch
+// values are sorted on the stack (no heap allocation).
 static bool any_repeat(const int32_t* v, int64_t n) {
   if (n < 2) return false;
+  if (n <= kMaxBatch) {
+    int32_t s[kMaxBatch];
+    std::copy(v, v + n, s);
+    std::sort(s, s + n);
+    return std::adjacent_find(s, s + n) != s + n;
+  }
   std::vector<int32_t> s(v, v + n);
   std::sort(s.begin(), s.end());
   return std::adjacent_find(s.begin(), s.end()) != s.end();
@@ -225,6 +233,52 @@ class DeviceScope {
 
 }  // namespace
 
+// Staging of kvx_cache_save_noalloc, for callers that cannot allocate device
+// memory. Every device that runs the library holds its own copy of this
+// array, at its own address, until the process ends. In host code the name
+// `scratch` is only a host-side stand-in: kernels and copies get the device
+// address that scratch_setup() looks up per device.
+static __device__ __align__(256) uint8_t scratch[KVX_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+
+struct ScratchTable {
+  std::mutex mu;
+  bool looked_up[kMaxScratchDevices] = {};
+  int status[kMaxScratchDevices] = {};        // KVX_OK, or the code of a failed lookup
+  uint8_t* address[kMaxScratchDevices] = {};  // device address of `scratch` on each device
+};
+
+ScratchTable g_scratch;
+
+// Looks up `scratch` on `device`, which must be current; once per device.
+// Writes the device's address (nullptr if the lookup failed) and status.
+void scratch_setup(int device, uint8_t** address, int* status) {
+  *address = nullptr;
+  if (device < 0 || device >= kMaxScratchDevices) {
+    *status = set_error(KVX_E_UNSUPPORTED, "static staging supports devices 0..%d", kMaxScratchDevices - 1);
+    return;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch.mu);
+  if (!g_scratch.looked_up[device]) {
+    void* p = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess) {
+      (void)hipGetLastError();  // leave no error behind for the caller's next HIP call
+      g_scratch.status[device] = (int)err;
+    } else {
+      g_scratch.address[device] = (uint8_t*)p;
+    }
+    g_scratch.looked_up[device] = true;
+  }
+  *address = g_scratch.address[device];
+  *status = g_scratch.status[device];
+}
+
+}  // namespace
+
 struct kvx_cache {
   int device = 0;
   uint8_t* pool = nullptr;
@@ -246,6 +300,14 @@ struct kvx_cache {
   bool host_reads_ok = false;  // restores may read host slots with the striding kernel
   int64_t saved = 0, restored = 0, waits = 0;
   int32_t debug = 0;  // KVX_DEBUG_* negative-control flags
+  // kvx_cache_save_noalloc: the device's static staging and the status of its
+  // lookup, and the one event every such save records (created with the
+  // cache and never returned to the pool). Saves run in order on the save
+  // stream, so a later record of this event completes after every earlier
+  // one: waiting for its latest record orders at least as strongly.
+  uint8_t* static_staging = nullptr;
+  int static_staging_status = KVX_E_STATE;
+  Event* static_done = nullptr;
 
   uint8_t* host_entry(int32_t slot) const {
     for (const Slab& s : slabs)
@@ -267,6 +329,9 @@ struct kvx_cache {
         return hip_status(err, "hipEventCreateWithFlags");
       }
       all_events.push_back(e);
+      // unref() returns events with push_back: with this capacity it never
+      // reallocates, so calls that create no event allocate nothing.
+      free_events.reserve(all_events.size());
     }
     e->refs = 0;
     *out = e;
@@ -322,7 +387,8 @@ struct kvx_cache {
   }
 
   // `save`: the slots are destinations and must be distinct; otherwise the blocks are.
-  int check_lists(bool save, const int32_t* ids, const int32_t* slots, int32_t n) const {
+  // `staged`: the call uses the attached staging.
+  int check_lists(bool save, const int32_t* ids, const int32_t* slots, int32_t n, bool staged = true) const {
     if (n < 0) return set_error(KVX_E_INVALID, "negative block count");
     if (n > 0 && (!ids || !slots)) return set_error(KVX_E_INVALID, "NULL block id or slot array");
     for (int32_t i = 0; i < n; ++i) {
@@ -333,7 +399,7 @@ struct kvx_cache {
     }
     if (any_repeat(save ? slots : ids, n))
       return set_error(KVX_E_INVALID, save ? "a slot appears twice in one save" : "a block appears twice in one restore");
-    if (n > 0 && !save_staging) return set_error(KVX_E_STATE, "no staging attached");
+    if (n > 0 && staged && !save_staging) return set_error(KVX_E_STATE, "no staging attached");
     return KVX_OK;
   }
 
@@ -440,7 +506,75 @@ struct kvx_cache {
   }
 
   int chunk() const { return std::min(staging_entries, kMaxBatch); }
+
+  // Entries the static staging holds (at most kMaxBatch: one launch).
+  int32_t static_entries() const {
+    return (int32_t)std::min<int64_t>(kMaxBatch, (int64_t)KVX_NOALLOC_SCRATCH_BYTES / entry_stride);
+  }
 };
+
+// The body of kvx_cache_save and kvx_cache_save_noalloc. `staging` holds
+// `staging_entries` entries; `fixed_done` (if set) is recorded instead of a
+// pooled event. Allocates nothing when fixed_done is set.
+static int save_blocks_to_slots(kvx_cache* c, const int32_t* ids, const int32_t* slots, int32_t n,
+                                hipStream_t compute, uint8_t* staging, int32_t staging_entries,
+                                Event* fixed_done) {
+  DeviceScope scope;
+  int rc = scope.enter(c->device);
+  if (rc) return rc;
+  hipStream_t s = c->save_stream;
+  // Start after the kernels that wrote these blocks (cpu_prefix_cache.py:310-311).
+  bool caller_busy = false;
+  rc = c->wait_stream(s, compute, &caller_busy);
+  if (rc) return rc;
+  // With split streams, after the last restore that read each target slot (:312-314).
+  if (c->split && !(c->debug & KVX_DEBUG_SKIP_SLOT_READ_WAIT)) {
+    for (int32_t i = 0; i < n; ++i) {
+      Event*& r = c->slot_read[slots[i]];
+      if (r) {
+        rc = c->wait_event(s, r);
+        if (rc) return rc;
+        c->unref(r);
+      }
+    }
+  }
+  // After a background restore still writing a source block (a prefetched
+  // block whose CPU entry was dropped can be saved again before first use).
+  if (c->split) {
+    for (int32_t i = 0; i < n; ++i) {
+      if (Event* pr = c->pending_restore[ids[i]]) {
+        rc = c->wait_event(s, pr);
+        if (rc) return rc;
+      }
+    }
+  }
+  if (kvx_cache::direct_save(n, caller_busy)) {
+    rc = c->launch(true, ids, nullptr, slots, n, s);
+    if (rc) return rc;
+  } else {
+    const int32_t step = std::min(staging_entries, kMaxBatch);
+    for (int32_t base = 0; base < n; base += step) {
+      const int32_t cnt = std::min(step, n - base);
+      rc = c->launch(true, ids + base, staging, nullptr, cnt, s);
+      if (!rc) rc = c->dma(true, staging, slots + base, cnt, s);
+      if (rc) return rc;
+    }
+  }
+  Event* done = fixed_done;
+  if (!done) rc = c->new_event(&done);
+  if (!rc) rc = hip_status(hipEventRecord(done->ev, s), "hipEventRecord");
+  if (rc) {
+    if (done && !fixed_done) c->release_if_unused(done);
+    return rc;
+  }
+  for (int32_t i = 0; i < n; ++i) {
+    c->assign(c->pending_save[ids[i]], done);
+    c->assign(c->slot_saved[slots[i]], done);
+  }
+  c->assign(c->last_save, done);
+  c->saved += n;
+  return KVX_OK;
+}
 
 extern "C" {
 
@@ -541,10 +675,15 @@ int kvx_cache_create(void* pool, const kvx_block_layout* layout, int32_t format,
   DeviceScope scope;
   rc = scope.enter(device);
   if (!rc) rc = hip_status(hipEventCreateWithFlags(&c->marker, hipEventDisableTiming), "hipEventCreate");
+  if (!rc) rc = c->new_event(&c->static_done);
   if (rc) {
     kvx_cache_destroy(c);
     return rc;
   }
+  c->static_done->refs = 1;  // held by the cache: never returns to the event pool
+  // Set-up for kvx_cache_save_noalloc, with the device current. A failed
+  // lookup fails only that entry point, which reports it.
+  scratch_setup(device, &c->static_staging, &c->static_staging_status);
   *out = c;
   return KVX_OK;
 }
@@ -618,61 +757,24 @@ int kvx_cache_save(kvx_cache* c, const int32_t* ids, const int32_t* slots, int32
   if (!c) return set_error(KVX_E_INVALID, "NULL cache");
   int rc = c->check_lists(true, ids, slots, n);
   if (rc || n == 0) return rc;
-  DeviceScope scope;
-  rc = scope.enter(c->device);
-  if (rc) return rc;
-  hipStream_t s = c->save_stream;
-  // Start after the kernels that wrote these blocks (cpu_prefix_cache.py:310-311).
-  bool caller_busy = false;
-  rc = c->wait_stream(s, (hipStream_t)compute_stream, &caller_busy);
-  if (rc) return rc;
-  // With split streams, after the last restore that read each target slot (:312-314).
-  if (c->split && !(c->debug & KVX_DEBUG_SKIP_SLOT_READ_WAIT)) {
-    for (int32_t i = 0; i < n; ++i) {
-      Event*& r = c->slot_read[slots[i]];
-      if (r) {
-        rc = c->wait_event(s, r);
-        if (rc) return rc;
-        c->unref(r);
-      }
-    }
-  }
-  // After a background restore still writing a source block (a prefetched
-  // block whose CPU entry was dropped can be saved again before first use).
-  if (c->split) {
-    for (int32_t i = 0; i < n; ++i) {
-      if (Event* pr = c->pending_restore[ids[i]]) {
-        rc = c->wait_event(s, pr);
-        if (rc) return rc;
-      }
-    }
-  }
-  if (kvx_cache::direct_save(n, caller_busy)) {
-    rc = c->launch(true, ids, nullptr, slots, n, s);
-    if (rc) return rc;
-  } else {
-    const int32_t step = c->chunk();
-    for (int32_t base = 0; base < n; base += step) {
-      const int32_t cnt = std::min(step, n - base);
-      rc = c->launch(true, ids + base, c->save_staging, nullptr, cnt, s);
-      if (!rc) rc = c->dma(true, c->save_staging, slots + base, cnt, s);
-      if (rc) return rc;
-    }
-  }
-  Event* done = nullptr;
-  rc = c->new_event(&done);
-  if (!rc) rc = hip_status(hipEventRecord(done->ev, s), "hipEventRecord");
-  if (rc) {
-    if (done) c->release_if_unused(done);
-    return rc;
-  }
-  for (int32_t i = 0; i < n; ++i) {
-    c->assign(c->pending_save[ids[i]], done);
-    c->assign(c->slot_saved[slots[i]], done);
-  }
-  c->assign(c->last_save, done);
-  c->saved += n;
-  return KVX_OK;
+  return save_blocks_to_slots(c, ids, slots, n, (hipStream_t)compute_stream, c->save_staging, c->staging_entries,
+                              nullptr);
+}
+
+int kvx_cache_save_noalloc(kvx_cache* c, const int32_t* ids, const int32_t* slots, int32_t n,
+                           void* compute_stream) {
+  if (!c) return set_error(KVX_E_INVALID, "NULL cache");
+  int rc = c->check_lists(true, ids, slots, n, false);
+  if (rc || n == 0) return rc;
+  if (c->static_staging_status != KVX_OK || !c->static_staging || !c->static_done)
+    return set_error(c->static_staging_status != KVX_OK ? c->static_staging_status : KVX_E_STATE,
+                     "no static staging on device %d", c->device);
+  const int32_t max_n = c->static_entries();
+  if (n > max_n)
+    return set_error(KVX_E_RANGE, "%d blocks exceed the static staging: at most %d entries of %lld bytes fit in %lld "
+                     "bytes", n, max_n, (long long)c->entry_stride, (long long)KVX_NOALLOC_SCRATCH_BYTES);
+  return save_blocks_to_slots(c, ids, slots, n, (hipStream_t)compute_stream, c->static_staging, max_n,
+                              c->static_done);
 }
 
 int kvx_cache_restore(kvx_cache* c, const int32_t* slots, const int32_t* ids, int32_t n, int32_t wait,

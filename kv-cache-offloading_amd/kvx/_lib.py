@@ -20,6 +20,7 @@ E_INVALID, E_RANGE, E_STATE, E_UNSUPPORTED = -1, -2, -3, -4
 SCALE_BF16, SCALE_FP32 = 0, 1
 FORMAT_RAW, FORMAT_FP8 = 0, 1
 DEBUG_SKIP_SAVE_WAIT, DEBUG_SKIP_SLOT_READ_WAIT, DEBUG_SKIP_REUSE_WAIT, DEBUG_SKIP_VICTIM_WAIT = 1, 2, 4, 8
+NOALLOC_SCRATCH_BYTES = 64 << 20  # KVX_NOALLOC_SCRATCH_BYTES
 
 _c_p = ctypes.c_void_p
 _i32, _i64 = ctypes.c_int32, ctypes.c_int64
@@ -63,6 +64,7 @@ SIGNATURES = {
     "kvx_cache_reset_slabs": (_i32, [_c_p]),
     "kvx_cache_streams": (_i32, [_c_p, ctypes.POINTER(_c_p), ctypes.POINTER(_c_p)]),
     "kvx_cache_save": (_i32, [_c_p, ctypes.POINTER(_i32), ctypes.POINTER(_i32), _i32, _c_p]),
+    "kvx_cache_save_noalloc": (_i32, [_c_p, ctypes.POINTER(_i32), ctypes.POINTER(_i32), _i32, _c_p]),
     "kvx_cache_restore": (_i32, [_c_p, ctypes.POINTER(_i32), ctypes.POINTER(_i32), _i32, _i32, _c_p]),
     "kvx_cache_before_block_reuse": (_i32, [_c_p, _i32, _c_p]),
     "kvx_cache_before_block_use": (_i32, [_c_p, _i32, _c_p]),
