@@ -207,7 +207,7 @@ def store_beside_saves(torch, ops, pool, key, value, lengths, reps):
 
     from kvx.engine.block_manager import BlockManager
     from kvx.engine.cpu_prefix_cache import CPUBlockCache
-    from kvx.workloads import block_selection
+    from workloads import block_selection
 
     _, layers, nb, bs, heads, hd = pool.shape
     evicted = block_selection(nb, 64, seed=6)
@@ -287,7 +287,7 @@ def microbench_leg(torch, blocks=64, matmul_iters=200):
 
     from kvx.engine.block_manager import BlockManager
     from kvx.engine.cpu_prefix_cache import CPUBlockCache
-    from kvx.workloads import QWEN3_0_6B
+    from workloads import QWEN3_0_6B
 
     n = blocks
     shape = (2, QWEN3_0_6B.layers, 2 * n, *QWEN3_0_6B.shape[3:])
@@ -446,7 +446,7 @@ def agent_leg(torch, pool, scale_dtype):
     from contextlib import nullcontext
 
     from kvx.engine.llm_engine import LLMEngine
-    from kvx.workloads import SyntheticKVRunner, run_agent_pressure
+    from workloads import SyntheticKVRunner, run_agent_pressure
 
     out = {"agents": 4, "context_tokens": 32768, "turns": 12, "append_tokens": 2048, "host_budget_bytes": 8 << 30}
     # The first (untimed, one-turn) run grows torch's allocator for the synthetic model, so no timed run pays it.
@@ -599,7 +599,7 @@ def handoff_leg(torch, pool, reps=3):
     index_select, pack, .cpu(); :112-118: .to(device), one copy_ per block).
     """
     from kvx import ops
-    from kvx.workloads import block_selection
+    from workloads import block_selection
 
     _, layers, nb, bs, heads, hd = pool.shape
     count = 128 * bs - 1
@@ -653,7 +653,7 @@ def handoff_leg(torch, pool, reps=3):
 def bf16_leg(torch, ops, pool, reps, link=True):
     """BF16 storage mode on the Qwen3-8B pool: byte gather of 200 seeded blocks into entries and scatter into a
     seeded permutation of the pool (HBM-resident), then 128 + 128 blocks over the host link."""
-    from kvx.workloads import block_selection
+    from workloads import block_selection
 
     nb = pool.shape[2]
     sources = block_selection(nb, 200, seed=3)
@@ -679,7 +679,7 @@ def bf16_leg(torch, ops, pool, reps, link=True):
 
 def qwen3_0_6b_leg(torch, ops, scale_dtype):
     """FP8 save of 16 seeded Qwen3-0.6B blocks and restore into 16 other seeded blocks, HBM-resident."""
-    from kvx.workloads import QWEN3_0_6B, block_selection, fill_normal
+    from workloads import QWEN3_0_6B, block_selection, fill_normal
 
     pool = torch.empty(QWEN3_0_6B.shape, dtype=torch.bfloat16, device="cuda")
     fill_normal(pool, seed=0)
@@ -893,7 +893,7 @@ def main():
     import torch
 
     from kvx import ops
-    from kvx.workloads import QWEN3_8B, block_selection, fill_student_t
+    from workloads import QWEN3_8B, block_selection, fill_student_t
 
     if not torch.cuda.is_available():
         sys.exit("bench.py needs a ROCm GPU")

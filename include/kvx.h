@@ -144,6 +144,25 @@ int kvx_scatter_tokens(void* pool, const kvx_block_layout* layout, const int32_t
                        int32_t table_len, int64_t num_rows, const void* src, void* stream);
 
 /*
+ * FP8 KV handoff: the token copies above with the FP8 codec. A sequence's
+ * first num_rows rows of the blocks block_table_host[0..] correspond to a
+ * dense e4m3 payload [planes][num_rows][head_dim] and a dense scale array
+ * [planes][num_rows] of layout->scale_dtype. kvx_gather_tokens_fp8 writes
+ * them with fp8_quantize's arithmetic (nanovllm/engine/cpu_prefix_cache.py:
+ * 20-24), i.e. what fp8_quantize gives for export_kv's BF16 payload
+ * (nanovllm/engine/kv_handoff.py:46-55), at half its bytes on the wire;
+ * kvx_scatter_tokens_fp8 dequantises them into the blocks (:27-28), in place
+ * of import_kv's per-block copy (kv_handoff.py:112-118). Payload and scales
+ * may be device memory or, for the gather, pinned host memory; they may not
+ * overlap; a scatter's table may not name a block twice (KVX_E_INVALID).
+ */
+int kvx_gather_tokens_fp8(const void* pool, const kvx_block_layout* layout, const int32_t* block_table_host,
+                          int32_t table_len, int64_t num_rows, void* payload, void* scales, void* stream);
+int kvx_scatter_tokens_fp8(void* pool, const kvx_block_layout* layout, const int32_t* block_table_host,
+                           int32_t table_len, int64_t num_rows, const void* payload, const void* scales,
+                           void* stream);
+
+/*
  * Copy engine: the stream/event half of CPUBlockCache
  * (nanovllm/engine/cpu_prefix_cache.py:72-131, 270-273, 306-322, 352-363,
  * 370-398). It queues copies on a save stream and a restore stream that the

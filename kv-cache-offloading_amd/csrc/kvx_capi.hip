@@ -190,6 +190,53 @@ static int token_copy(bool gather, void* pool, const kvx_block_layout* l, const 
   return KVX_OK;
 }
 
+// Token-granular FP8 copy between the blocks in `table` and a dense
+// [planes][num_rows][hd] e4m3 payload with one scale per row in a dense
+// [planes][num_rows] array.
+static int token_fp8(bool gather, void* pool, const kvx_block_layout* l, const int32_t* table, int32_t table_len,
+                     int64_t num_rows, void* payload, void* scales, hipStream_t stream) {
+  int rc = check_layout(l, KVX_FORMAT_FP8);
+  if (rc) return rc;
+  if (num_rows < 0 || table_len < 0) return set_error(KVX_E_INVALID, "negative row or block count");
+  if (num_rows == 0) return KVX_OK;
+  if (!pool || !payload || !scales || !table) return set_error(KVX_E_INVALID, "NULL pool, payload, scales or table");
+  const int64_t sb = l->scale_dtype == KVX_SCALE_BF16 ? 2 : 4;
+  if ((uintptr_t)pool % 2) return set_error(KVX_E_INVALID, "pool is not 2-byte aligned");
+  if ((uintptr_t)scales % (uintptr_t)sb) return set_error(KVX_E_INVALID, "scales are not %lld-byte aligned", (long long)sb);
+  const int64_t R = l->plane_rows, hd = l->head_dim;
+  const int64_t nblocks = (num_rows + R - 1) / R;
+  if (nblocks > table_len)
+    return set_error(KVX_E_RANGE, "%lld rows need %lld blocks, the table has %d", (long long)num_rows,
+                     (long long)nblocks, table_len);
+  for (int64_t i = 0; i < nblocks; ++i)
+    if (table[i] < 0 || table[i] >= l->num_blocks)
+      return set_error(KVX_E_RANGE, "block id %d outside [0, %d)", table[i], l->num_blocks);
+  if (!gather && any_repeat(table, nblocks)) return set_error(KVX_E_INVALID, "a block appears twice in one scatter");
+  const uintptr_t p0 = (uintptr_t)payload, s0 = (uintptr_t)scales;
+  const uintptr_t payload_bytes = (uintptr_t)(l->planes * num_rows * hd), scale_bytes = (uintptr_t)(l->planes * num_rows * sb);
+  if (gather && p0 < s0 + scale_bytes && s0 < p0 + payload_bytes)
+    return set_error(KVX_E_INVALID, "payload and scales overlap");
+  // Vector kernels store scales 16 bytes at a time from tile-aligned rows.
+  const bool aligned = p0 % 16 == 0 && s0 % 16 == 0 && (num_rows * hd) % 16 == 0 && (num_rows * sb) % 16 == 0 &&
+                       (R * sb) % 16 == 0;
+  TokenSpan span{num_rows * hd, num_rows * sb, R * (sb - hd), (int32_t)R};
+  BlockBatch b;
+  for (int64_t base = 0; base < nblocks; base += kMaxBatch) {
+    b.n = (int32_t)std::min<int64_t>(kMaxBatch, nblocks - base);
+    for (int32_t i = 0; i < b.n; ++i) {
+      b.ids[i] = table[base + i];
+      b.entries[i] = (uint64_t)(p0 + (uintptr_t)((base + i) * R * hd));
+    }
+    span.last_rows = (int32_t)(base + b.n == nblocks ? num_rows - (nblocks - 1) * R : R);
+    // Entry i's scales: scales + (base + i) * R * sb = entries[i] + scale_offset + i * scale_entry_step.
+    const int64_t scale_offset = (int64_t)(s0 + (uintptr_t)(base * R * sb)) - (int64_t)(p0 + (uintptr_t)(base * R * hd));
+    const bool vec = aligned && vector_access_ok(pool, *l, b.entries, b.n);
+    hipError_t err = launch_token_fp8(gather, pool, *l, b, scale_offset, span, vec, stream);
+    if (err != hipSuccess) return hip_status(err, gather ? "FP8 token gather launch" : "FP8 token scatter launch");
+  }
+  return KVX_OK;
+}
+
 }  // namespace kvx
 
 using namespace kvx;
@@ -635,6 +682,19 @@ int kvx_scatter_tokens(void* pool, const kvx_block_layout* layout, const int32_t
                        int32_t table_len, int64_t num_rows, const void* src, void* stream) {
   return token_copy(false, pool, layout, block_table_host, table_len, num_rows, const_cast<void*>(src),
                     (hipStream_t)stream);
+}
+
+int kvx_gather_tokens_fp8(const void* pool, const kvx_block_layout* layout, const int32_t* block_table_host,
+                          int32_t table_len, int64_t num_rows, void* payload, void* scales, void* stream) {
+  return token_fp8(true, const_cast<void*>(pool), layout, block_table_host, table_len, num_rows, payload, scales,
+                   (hipStream_t)stream);
+}
+
+int kvx_scatter_tokens_fp8(void* pool, const kvx_block_layout* layout, const int32_t* block_table_host,
+                           int32_t table_len, int64_t num_rows, const void* payload, const void* scales,
+                           void* stream) {
+  return token_fp8(false, pool, layout, block_table_host, table_len, num_rows, const_cast<void*>(payload),
+                   const_cast<void*>(scales), (hipStream_t)stream);
 }
 
 int kvx_sleep(void* stream, int64_t microseconds) {

@@ -19,15 +19,37 @@ struct BlockBatch {
   uint64_t entries[kMaxBatch];
 };
 
-// Launch-time geometry derived from kvx_block_layout.
+// Launch-time geometry derived from kvx_block_layout. For FP8 entries, the
+// payload of (entry e, plane p, row r) is at
+//   entries[e] + p * payload_plane_stride + r * head_dim
+// and its scale at
+//   entries[e] + scale_offset + e * scale_entry_step + p * scale_plane_stride + r * scale_bytes.
+// Block entries are dense per block (payload_plane_stride = plane_rows *
+// head_dim, scale_plane_stride = plane_rows * scale_bytes, no entry step);
+// token entries (KV handoff) are one block's rows of a [planes][rows][hd]
+// payload and a [planes][rows] scale array. The batch's last entry has
+// last_rows valid rows per plane (a sequence's partial final block), the
+// others plane_rows.
 struct PlaneGeom {
   int64_t plane_stride;  // elements
   int64_t block_stride;  // elements
   int64_t scale_offset;  // bytes from an entry's payload to its scales
+  int64_t payload_plane_stride;  // bytes (FP8)
+  int64_t scale_plane_stride;    // bytes (FP8)
+  int64_t scale_entry_step;      // bytes (FP8)
   int32_t planes;
   int32_t plane_rows;
+  int32_t last_rows;
   int32_t head_dim;
   int32_t chunks;        // tiles per plane
+};
+
+// FP8 token entries of one launch (see PlaneGeom).
+struct TokenSpan {
+  int64_t payload_plane_stride;
+  int64_t scale_plane_stride;
+  int64_t scale_entry_step;
+  int32_t last_rows;
 };
 
 // Records a message for kvx_last_error() and returns `code`.
@@ -59,6 +81,10 @@ bool striding_restore_supported(const kvx_block_layout& layout, int32_t format, 
 // batch's last block copies last_bytes per plane.
 hipError_t launch_token_copy(bool gather, void* pool, const kvx_block_layout& layout, const BlockBatch& batch,
                              bool vector_ok, int64_t dense_plane_stride, int64_t last_bytes, hipStream_t stream);
+// The same with FP8 quantisation (gather) or dequantisation (scatter):
+// entries are the payload rows of each block, scales per `span`.
+hipError_t launch_token_fp8(bool gather, void* pool, const kvx_block_layout& layout, const BlockBatch& batch,
+                            int64_t scale_offset, const TokenSpan& span, bool vector_ok, hipStream_t stream);
 // True when 16-byte vector kernels may address this pool/entry combination.
 bool vector_access_ok(const void* pool, const kvx_block_layout& layout, const uint64_t* entries, int32_t n);
 hipError_t launch_store_kvcache(const void* key, int64_t key_stride, const void* value,

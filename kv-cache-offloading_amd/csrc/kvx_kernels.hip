@@ -324,17 +324,17 @@ __global__ __launch_bounds__(kBlock) void fp8_save_kernel(const uint16_t* __rest
   const int lane = threadIdx.x % M::kLanes;
   const int rsub = threadIdx.x / M::kLanes;
   const int row = tc.row0 + rsub;
-  const bool full = tc.row0 + kRows <= g.plane_rows;
+  const int rows = tc.entry == b.n - 1 ? g.last_rows : g.plane_rows;  // valid rows of this plane
+  const bool full = tc.row0 + kRows <= rows;
   const uint16_t* src = pool + (int64_t)b.ids[tc.entry] * g.block_stride + (int64_t)tc.plane * g.plane_stride;
-  uint8_t* payload = reinterpret_cast<uint8_t*>(b.entries[tc.entry]) + (int64_t)tc.plane * g.plane_rows * kHd;
+  uint8_t* payload = reinterpret_cast<uint8_t*>(b.entries[tc.entry]) + (int64_t)tc.plane * g.payload_plane_stride;
   uint8_t* scales = reinterpret_cast<uint8_t*>(b.entries[tc.entry]) + g.scale_offset +
-                    (int64_t)tc.plane * g.plane_rows * kScaleBytes;
+                    (int64_t)tc.entry * g.scale_entry_step + (int64_t)tc.plane * g.scale_plane_stride;
 
   uint4 x[kVec];
 #pragma unroll
   for (int v = 0; v < kVec; ++v)
-    x[v] = row < g.plane_rows ? load_nt16(src + (int64_t)row * kHd + v * (kHd / kVec) + lane * 8)
-                              : make_uint4(0, 0, 0, 0);
+    x[v] = row < rows ? load_nt16(src + (int64_t)row * kHd + v * (kHd / kVec) + lane * 8) : make_uint4(0, 0, 0, 0);
   uint32_t m = amax8(x[0]);
 #pragma unroll
   for (int v = 1; v < kVec; ++v) {
@@ -353,11 +353,11 @@ __global__ __launch_bounds__(kBlock) void fp8_save_kernel(const uint16_t* __rest
   __syncthreads();
   uint8_t* tile_payload = payload + (int64_t)tc.row0 * kHd;
   for (int i = threadIdx.x; i < kRows * kHd / 16; i += kBlock)
-    if (full || tc.row0 + i * 16 / kHd < g.plane_rows) store16<kStride>(tile_payload + i * 16, codes[i]);
+    if (full || tc.row0 + i * 16 / kHd < rows) store16<kStride>(tile_payload + i * 16, codes[i]);
   if (full) {
     for (int i = threadIdx.x; i < kRows * kScaleBytes / 16; i += kBlock)
       store16<kStride>(scales + (int64_t)tc.row0 * kScaleBytes + i * 16, scale_tile[i]);
-  } else if (lane == 0 && row < g.plane_rows) {  // ragged last tile of a plane
+  } else if (lane == 0 && row < rows) {  // ragged last tile of a plane
     if (kScaleBf16) reinterpret_cast<uint16_t*>(scales)[row] = (uint16_t)r.bits;
     else reinterpret_cast<uint32_t*>(scales)[row] = r.bits;
   }
@@ -386,27 +386,28 @@ __global__ __launch_bounds__(kBlock) void fp8_restore_kernel(uint16_t* __restric
   const int lane = threadIdx.x % M::kLanes;
   const int rsub = threadIdx.x / M::kLanes;
   const int row = tc.row0 + rsub;
+  const int rows = tc.entry == b.n - 1 ? g.last_rows : g.plane_rows;  // valid rows of this plane
   uint16_t* dst = pool + (int64_t)b.ids[tc.entry] * g.block_stride + (int64_t)tc.plane * g.plane_stride;
   const uint8_t* payload =
-      reinterpret_cast<const uint8_t*>(b.entries[tc.entry]) + (int64_t)tc.plane * g.plane_rows * kHd;
+      reinterpret_cast<const uint8_t*>(b.entries[tc.entry]) + (int64_t)tc.plane * g.payload_plane_stride;
   const uint8_t* scales = reinterpret_cast<const uint8_t*>(b.entries[tc.entry]) + g.scale_offset +
-                          (int64_t)tc.plane * g.plane_rows * (kScaleBf16 ? 2 : 4);
+                          (int64_t)tc.entry * g.scale_entry_step + (int64_t)tc.plane * g.scale_plane_stride;
 
   const uint8_t* tile_codes = payload + (int64_t)tc.row0 * kHd;
   float s = 0.0f;
   if (kStride) {  // entries in host memory
-    const int tile_bytes = (g.plane_rows - tc.row0 < kRows ? g.plane_rows - tc.row0 : kRows) * kHd;
+    const int left = rows - tc.row0;
+    const int tile_bytes = (left < 0 ? 0 : left < kRows ? left : kRows) * kHd;
     const __amdgpu_buffer_rsrc_t rc = host_rsrc(tile_codes, tile_bytes);
     for (int i = threadIdx.x; i < kPieces; i += kBlock) codes[i] = load_host16(rc, i * 16);
-    if (row < g.plane_rows)
-      s = scale_value_host(host_rsrc(scales, (int64_t)g.plane_rows * (kScaleBf16 ? 2 : 4)), row, kScaleBf16);
+    if (row < rows) s = scale_value_host(host_rsrc(scales, (int64_t)rows * (kScaleBf16 ? 2 : 4)), row, kScaleBf16);
   } else {
     for (int i = threadIdx.x; i < kPieces; i += kBlock)
-      codes[i] = tc.row0 + i * 16 / kHd < g.plane_rows ? load_nt16(tile_codes + i * 16) : make_uint4(0, 0, 0, 0);
-    if (row < g.plane_rows) s = scale_value(scales, row, kScaleBf16);
+      codes[i] = tc.row0 + i * 16 / kHd < rows ? load_nt16(tile_codes + i * 16) : make_uint4(0, 0, 0, 0);
+    if (row < rows) s = scale_value(scales, row, kScaleBf16);
   }
   __syncthreads();
-  if (row < g.plane_rows) {
+  if (row < rows) {
     const uint2* code_words = reinterpret_cast<const uint2*>(codes);
 #pragma unroll
     for (int v = 0; v < kVec; ++v) {
@@ -429,7 +430,7 @@ __device__ __forceinline__ bool generic_row(const PlaneGeom& g, int n, int64_t& 
   const int64_t rem = idx - entry * per_entry;
   plane = rem / g.plane_rows;
   row = rem - plane * g.plane_rows;
-  return true;
+  return row < (entry == n - 1 ? g.last_rows : g.plane_rows);
 }
 
 template <bool kScaleBf16>
@@ -439,9 +440,9 @@ __global__ __launch_bounds__(kThreads) void fp8_save_generic(const uint16_t* __r
   if (!generic_row(g, b.n, e, p, row)) return;
   const int hd = g.head_dim;
   const uint16_t* src = pool + (int64_t)b.ids[e] * g.block_stride + p * g.plane_stride + row * hd;
-  const int64_t r_global = p * g.plane_rows + row;
-  uint8_t* payload = reinterpret_cast<uint8_t*>(b.entries[e]) + r_global * hd;
-  uint8_t* scales = reinterpret_cast<uint8_t*>(b.entries[e]) + g.scale_offset;
+  uint8_t* payload = reinterpret_cast<uint8_t*>(b.entries[e]) + p * g.payload_plane_stride + row * hd;
+  uint8_t* scales = reinterpret_cast<uint8_t*>(b.entries[e]) + g.scale_offset + e * g.scale_entry_step +
+                    p * g.scale_plane_stride;
   uint32_t m = 0;
   for (int i = 0; i < hd; ++i) {
     uint32_t a = src[i] & 0x7FFFu;
@@ -455,8 +456,8 @@ __global__ __launch_bounds__(kThreads) void fp8_save_generic(const uint16_t* __r
                            : code_slow(mag, r);
     payload[i] = (uint8_t)(code | ((h >> 8) & 0x80u));
   }
-  if (kScaleBf16) reinterpret_cast<uint16_t*>(scales)[r_global] = (uint16_t)r.bits;
-  else reinterpret_cast<uint32_t*>(scales)[r_global] = r.bits;
+  if (kScaleBf16) reinterpret_cast<uint16_t*>(scales)[row] = (uint16_t)r.bits;
+  else reinterpret_cast<uint32_t*>(scales)[row] = r.bits;
 }
 
 template <bool kScaleBf16>
@@ -466,10 +467,10 @@ __global__ __launch_bounds__(kThreads) void fp8_restore_generic(uint16_t* __rest
   if (!generic_row(g, b.n, e, p, row)) return;
   const int hd = g.head_dim;
   uint16_t* dst = pool + (int64_t)b.ids[e] * g.block_stride + p * g.plane_stride + row * hd;
-  const int64_t r_global = p * g.plane_rows + row;
-  const uint8_t* payload = reinterpret_cast<const uint8_t*>(b.entries[e]) + r_global * hd;
-  const uint8_t* scales = reinterpret_cast<const uint8_t*>(b.entries[e]) + g.scale_offset;
-  const float s = scale_value(scales, r_global, kScaleBf16);
+  const uint8_t* payload = reinterpret_cast<const uint8_t*>(b.entries[e]) + p * g.payload_plane_stride + row * hd;
+  const uint8_t* scales = reinterpret_cast<const uint8_t*>(b.entries[e]) + g.scale_offset + e * g.scale_entry_step +
+                          p * g.scale_plane_stride;
+  const float s = scale_value(scales, row, kScaleBf16);
   for (int i = 0; i < hd; ++i) {
     const float v = __builtin_amdgcn_cvt_f32_fp8((uint32_t)payload[i], 0);
     dst[i] = (uint16_t)(f32x2_to_bf16x2(v * s, 0.0f) & 0xFFFFu);
@@ -683,13 +684,20 @@ __global__ void zero_counters(uint64_t* c) {
 // ---------------------------------------------------------------------------
 // Launchers
 
-static PlaneGeom make_geom(const kvx_block_layout& l, int tile_rows, int64_t scale_offset) {
+// Geometry of block entries (dense per block); `span` switches FP8 entries to token entries.
+static PlaneGeom make_geom(const kvx_block_layout& l, int tile_rows, int64_t scale_offset,
+                           const TokenSpan* span = nullptr) {
   PlaneGeom g;
   g.plane_stride = l.plane_stride;
   g.block_stride = l.block_stride;
   g.scale_offset = scale_offset;
+  const int64_t scale_bytes = l.scale_dtype == KVX_SCALE_BF16 ? 2 : 4;
+  g.payload_plane_stride = span ? span->payload_plane_stride : (int64_t)l.plane_rows * l.head_dim;
+  g.scale_plane_stride = span ? span->scale_plane_stride : (int64_t)l.plane_rows * scale_bytes;
+  g.scale_entry_step = span ? span->scale_entry_step : 0;
   g.planes = l.planes;
   g.plane_rows = l.plane_rows;
+  g.last_rows = span ? span->last_rows : l.plane_rows;
   g.head_dim = l.head_dim;
   g.chunks = tile_rows > 0 ? (l.plane_rows + tile_rows - 1) / tile_rows : 0;
   return g;
@@ -699,7 +707,8 @@ static unsigned generic_grid(int64_t items) { return (unsigned)((items + kThread
 
 template <bool kScaleBf16>
 static hipError_t launch_fp8(bool save, void* pool, const kvx_block_layout& l, const BlockBatch& b,
-                             int64_t scale_offset, bool vector_ok, int32_t max_grid, hipStream_t stream) {
+                             int64_t scale_offset, bool vector_ok, int32_t max_grid, hipStream_t stream,
+                             const TokenSpan* span = nullptr) {
   // Workgroup sizes chosen by sweeps on the Qwen3-8B block workload: save
   // 128 threads (16 rows for hd=128), restore 64 threads (8 rows). A capped
   // (striding) restore reads host slots and needs more bytes in flight per
@@ -709,7 +718,7 @@ static hipError_t launch_fp8(bool save, void* pool, const kvx_block_layout& l, c
   constexpr int kRestoreStrideBlock = 256;
   auto run = [&](auto save_k, auto save_stride_k, auto restore_k, auto restore_stride_k, int lanes) -> hipError_t {
     const int block = save ? kSaveBlock : kRestoreBlock;
-    PlaneGeom g = make_geom(l, block / lanes, scale_offset);
+    PlaneGeom g = make_geom(l, block / lanes, scale_offset, span);
     const unsigned grid = (unsigned)(b.n * g.planes * g.chunks);
     if (save && max_grid > 0 && (unsigned)max_grid < grid) {
       hipLaunchKernelGGL(save_stride_k, dim3((unsigned)max_grid), dim3(kSaveBlock), 0, stream, (const uint16_t*)pool,
@@ -717,7 +726,7 @@ static hipError_t launch_fp8(bool save, void* pool, const kvx_block_layout& l, c
     } else if (save) {
       hipLaunchKernelGGL(save_k, dim3(grid), dim3(kSaveBlock), 0, stream, (const uint16_t*)pool, g, b);
     } else if (max_grid > 0) {
-      PlaneGeom gs = make_geom(l, kRestoreStrideBlock / lanes, scale_offset);
+      PlaneGeom gs = make_geom(l, kRestoreStrideBlock / lanes, scale_offset, span);
       const unsigned tiles = (unsigned)(b.n * gs.planes * gs.chunks);
       hipLaunchKernelGGL(restore_stride_k, dim3((unsigned)max_grid < tiles ? (unsigned)max_grid : tiles), dim3(kRestoreStrideBlock), 0,
                          stream, (uint16_t*)pool, gs, b);
@@ -743,7 +752,7 @@ static hipError_t launch_fp8(bool save, void* pool, const kvx_block_layout& l, c
                  fp8_restore_kernel<256, 2, kRestoreBlock, kScaleBf16, false>,
                  fp8_restore_kernel<256, 2, kRestoreStrideBlock, kScaleBf16, true>, RowMap<256, 2>::kLanes);
     default: {
-      PlaneGeom g = make_geom(l, 0, scale_offset);
+      PlaneGeom g = make_geom(l, 0, scale_offset, span);
       const unsigned grid = generic_grid((int64_t)b.n * l.planes * l.plane_rows);
       if (save)
         hipLaunchKernelGGL(fp8_save_generic<kScaleBf16>, dim3(grid), dim3(kThreads), 0, stream,
@@ -808,6 +817,14 @@ hipError_t launch_token_copy(bool gather, void* pool, const kvx_block_layout& l,
                              bool vector_ok, int64_t dense_plane_stride, int64_t last_bytes, hipStream_t stream) {
   if (b.n <= 0) return hipSuccess;
   return launch_raw(gather, pool, l, b, vector_ok, dense_plane_stride, last_bytes, 0, stream);
+}
+
+hipError_t launch_token_fp8(bool gather, void* pool, const kvx_block_layout& l, const BlockBatch& b,
+                            int64_t scale_offset, const TokenSpan& span, bool vector_ok, hipStream_t stream) {
+  if (b.n <= 0) return hipSuccess;
+  return l.scale_dtype == KVX_SCALE_BF16
+             ? launch_fp8<true>(gather, pool, l, b, scale_offset, vector_ok, 0, stream, &span)
+             : launch_fp8<false>(gather, pool, l, b, scale_offset, vector_ok, 0, stream, &span);
 }
 
 bool vector_access_ok(const void* pool, const kvx_block_layout& l, const uint64_t* entries, int32_t n) {

@@ -1,14 +1,13 @@
 """kvx: MI355X-native KV-block copy path (libkvx HIP kernels behind a C ABI).
 
-Module layout mirrors the reference package it drops into:
+Drop-ins for the reference package's copy path:
   kvx.layers.attention.store_kvcache        <- nanovllm.layers.attention.store_kvcache
   kvx.engine.cpu_prefix_cache.CPUBlockCache <- nanovllm.engine.cpu_prefix_cache.CPUBlockCache
-  kvx.engine.block_manager.BlockManager     <- nanovllm.engine.block_manager.BlockManager
-  kvx.engine.scheduler.Scheduler            <- nanovllm.engine.scheduler.Scheduler
-  kvx.engine.llm_engine.LLMEngine           <- nanovllm.engine.llm_engine.LLMEngine (model-free)
-  kvx.engine.kv_handoff                     <- nanovllm.engine.kv_handoff
-  kvx.engine.handoff_timing                 <- nanovllm.engine.handoff_timing
-  kvx.ops                                   the operator API (codec, block lists, test hooks)
+  kvx.engine.kv_handoff                     <- nanovllm.engine.kv_handoff (plus an FP8 payload)
+  kvx.ops                                   the operator API (codec, block lists, token copies, test hooks)
+Callers of the copy path, with the reference's hook contract and signatures:
+  kvx.engine.block_manager.BlockManager, kvx.engine.scheduler.Scheduler,
+  kvx.engine.llm_engine.LLMEngine (model-free), kvx.engine.slot_mapping
 """
 
-__version__ = "0.1.0"
+__version__ = "0.2.0"

@@ -57,6 +57,10 @@ SIGNATURES = {
                                   ctypes.POINTER(ctypes.c_uint64), _i32, _i64, _c_p]),
     "kvx_gather_tokens": (_i32, [_c_p, ctypes.POINTER(BlockLayout), ctypes.POINTER(_i32), _i32, _i64, _c_p, _c_p]),
     "kvx_scatter_tokens": (_i32, [_c_p, ctypes.POINTER(BlockLayout), ctypes.POINTER(_i32), _i32, _i64, _c_p, _c_p]),
+    "kvx_gather_tokens_fp8": (_i32, [_c_p, ctypes.POINTER(BlockLayout), ctypes.POINTER(_i32), _i32, _i64, _c_p, _c_p,
+                                     _c_p]),
+    "kvx_scatter_tokens_fp8": (_i32, [_c_p, ctypes.POINTER(BlockLayout), ctypes.POINTER(_i32), _i32, _i64, _c_p,
+                                      _c_p, _c_p]),
     "kvx_cache_create": (_i32, [_c_p, ctypes.POINTER(BlockLayout), _i32, _c_p, _c_p, _i32, ctypes.POINTER(_c_p)]),
     "kvx_cache_destroy": (_i32, [_c_p]),
     "kvx_cache_set_staging": (_i32, [_c_p, _c_p, _c_p, _i32]),

@@ -1,2 +1,2 @@
-"""Engine-side callers of the copy path: block manager, CPU block cache, scheduler, model-free engine,
-KV handoff and its phase timing."""
+"""Engine-side callers of the copy path (block manager, scheduler, model-free engine, slot mappings),
+the CPU block cache and the KV handoff."""

@@ -1,43 +1,70 @@
-"""Paged KV block allocator with chained prefix hashes and CPU-tier hooks.
+"""GPU block accounting for the paged KV pool, and the caller of the CPU tier's hooks.
 
-This is the caller surface of the copy path: it decides which GPU blocks are
-saved before recycling, which CPU hits are restored on admission or
-prefetched, and when compute must wait for a copy. It follows
-nanovllm/engine/block_manager.py (line citations below) hook for hook, so a
-CPUBlockCache from kvx.engine.cpu_prefix_cache (or any object with the same
-duck-typed hooks) plugs in unchanged.
+The pool has `num_blocks` physical blocks of `block_size` tokens. A block is
+*published* while its chained prefix hash maps to it in `hash_to_block_id`;
+a published block that no request references stays in the free order as a
+GPU prefix hit until it is recycled. A CPU tier (CPUBlockCache, or any object
+with the same duck-typed hooks) attached as `_cpu_prefix_cache` is told:
+
+  recycling a published block    _preserve_before_recycle(hash), before the
+                                 hash is dropped; then before_block_reuse(id)
+                                 unless the new contents are copied in by a
+                                 prefetch or manual restore
+  releasing a published block    _preserve_on_release(hash)
+  taking a reference on a hit    before_block_use(id)
+  planning an admission          _entry_for(hash, tokens) (a pure lookup)
+  admitting or prefetching a     _copy_entry(entry, id, wait): waited on
+  CPU hit                        admission, unwaited after a hybrid split and
+                                 for prefetches
+  prefilling up to a split span  before_block_use(id) for each block of the span
+
+These calls, their order and their arguments are the reference
+BlockManager's (nanovllm/engine/block_manager.py:97-183, 202-237, 266-347),
+so a cache written for one works under the other; tests/test_hook_contract.py
+replays scenarios recorded from the reference and requires identical traces.
+The bookkeeping itself is this module's own: the free order is an ordered
+set (constant-time removal and move-to-back instead of deque scans), a
+prefix lookup yields typed hits, and an admission undoes itself through a
+journal of the references it took.
+
+When the tier has coalesce() (kvx's CPUBlockCache), the admission, prefetch
+and release loops run inside it, so their copies reach the copy engine as
+batches; the order of hook calls is unchanged.
 """
 
-from collections import deque
+from collections.abc import Callable, Iterable, Sequence as TokenSequence
 from contextlib import nullcontext
-from collections.abc import Callable, Sequence as TokenSequence
+from typing import NamedTuple
 
 import numpy as np
 import xxhash
 
 from kvx.engine.sequence import Sequence
 
+_HASH_LIMIT = 1 << 64
+
 
 def plan_split(cpu_blocks: int, block_size: int, restore_s_per_block: float,
                recompute_s_per_token: float, recompute_s_per_token2: float) -> int:
-    """Leading CPU-hit blocks to recompute while the rest restore (block_manager.py:9-23).
+    """Leading CPU-hit blocks to recompute while the others restore (block_manager.py:9-23).
 
-    Returns the smallest k in [0, cpu_blocks] minimising
-    max(recompute(k * block_size), (cpu_blocks - k) * restore_s_per_block) with
-    recompute(t) = t * recompute_s_per_token + t^2 * recompute_s_per_token2.
+    Recomputing the head overlaps restoring the tail, so the admission costs
+    the slower of the two: max(recompute(k * block_size), (cpu_blocks - k) *
+    restore_s_per_block) with recompute(t) = t * recompute_s_per_token +
+    t^2 * recompute_s_per_token2. Returns the smallest minimising k.
     """
-    best_k, best_cost = 0, None
-    for k in range(cpu_blocks + 1):
-        tokens = k * block_size
-        recompute = tokens * recompute_s_per_token + tokens * tokens * recompute_s_per_token2
-        cost = max(recompute, (cpu_blocks - k) * restore_s_per_block)
-        if best_cost is None or cost < best_cost:
-            best_k, best_cost = k, cost
-    return best_k
+    a, b = recompute_s_per_token, recompute_s_per_token2
+
+    def admission_s(k: int) -> float:
+        t = k * block_size
+        return max(t * a + t * t * b, (cpu_blocks - k) * restore_s_per_block)
+
+    costs = [admission_s(k) for k in range(cpu_blocks + 1)]
+    return costs.index(min(costs))
 
 
 class Block:
-    """One physical GPU block (block_manager.py:26-44)."""
+    """Metadata of one physical block. `hash` is -1 unless the block was published."""
 
     __slots__ = ("block_id", "ref_count", "hash", "token_ids", "release_gen", "seq_index")
 
@@ -46,104 +73,217 @@ class Block:
         self.ref_count = 0
         self.hash = -1
         self.token_ids: list[int] = []
-        # Generation of the last owner release and the block's index there (MRU order).
-        self.release_gen = 0
-        self.seq_index = 0
+        self.release_gen = 0  # the deallocate() call that last released it (MRU order)
+        self.seq_index = 0    # its position in that request's block table
 
     def update(self, hash: int, token_ids: list[int]):
         self.hash = hash
         self.token_ids = token_ids
 
     def reset(self):
+        """Handed to a new owner: one reference, no contents."""
         self.ref_count = 1
         self.hash = -1
         self.token_ids = []
 
 
+class FreeOrder:
+    """Idle block ids in recycle order (front first): an insertion-ordered set.
+
+    Membership, removal, append and move-to-back are O(1); the reference's
+    deque needs a scan for each removal of a GPU hit taken from the middle.
+    """
+
+    __slots__ = ("_ids",)
+
+    def __init__(self, ids: Iterable[int] = ()):
+        self._ids: dict[int, None] = dict.fromkeys(ids)
+
+    def __len__(self):
+        return len(self._ids)
+
+    def __bool__(self):
+        return bool(self._ids)
+
+    def __iter__(self):
+        return iter(self._ids)
+
+    def __contains__(self, block_id):
+        return block_id in self._ids
+
+    def __getitem__(self, i: int) -> int:
+        if i == 0 and self._ids:
+            return next(iter(self._ids))
+        if i == -1 and self._ids:
+            return next(reversed(self._ids))
+        return list(self._ids)[i]
+
+    def __repr__(self):
+        return f"FreeOrder({list(self._ids)})"
+
+    def append(self, block_id: int):
+        if block_id in self._ids:
+            raise ValueError(f"block {block_id} is already free")
+        self._ids[block_id] = None
+
+    def appendleft(self, block_id: int):
+        if block_id in self._ids:
+            raise ValueError(f"block {block_id} is already free")
+        self._ids = {block_id: None, **self._ids}
+
+    def extend(self, block_ids: Iterable[int]):
+        for block_id in block_ids:
+            self.append(block_id)
+
+    def remove(self, block_id: int):
+        del self._ids[block_id]
+
+    def move_to_back(self, block_id: int):
+        del self._ids[block_id]
+        self._ids[block_id] = None
+
+    def popleft(self) -> int:
+        block_id = next(iter(self._ids))
+        del self._ids[block_id]
+        return block_id
+
+    def clear(self):
+        self._ids.clear()
+
+
+class PrefixHit(NamedTuple):
+    """One leading full block of a request found in the pool (block_id) or in the CPU tier (entry)."""
+
+    index: int
+    hash: int
+    tokens: list[int]
+    block_id: int | None
+    entry: object | None
+
+
+class _Taken:
+    """References an admission took, dropped again (newest first) if it fails."""
+
+    def __init__(self, manager: "BlockManager"):
+        self.manager = manager
+        self.ids: list[int] = []
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, kind, error, trace):
+        if kind is not None:
+            for block_id in reversed(self.ids):
+                self.manager._release_block(block_id)
+        return False
+
+
 class BlockManager:
+    """Allocation, prefix caching and CPU-tier hooks for one pool. `eviction`: "lru" or "mru"."""
 
     def __init__(self, num_blocks: int, block_size: int, eviction: str = "lru"):
         if eviction not in ("lru", "mru"):
             raise ValueError("eviction must be 'lru' or 'mru'")
+        if num_blocks <= 0 or block_size <= 0:
+            raise ValueError("num_blocks and block_size must be positive")
         self.block_size = block_size
         self.eviction = eviction
         self.blocks = [Block(i) for i in range(num_blocks)]
         self.hash_to_block_id: dict[int, int] = {}
-        self.free_block_ids: deque[int] = deque(range(num_blocks))
+        self._free = FreeOrder(range(num_blocks))
         self.used_block_ids: set[int] = set()
         self._cpu_prefix_cache = None
-        self._last_prefetch = None
-        self._release_gen = 0
-        # Idle blocks a blocked request's prefetch keeps (consulted by MRU eviction).
-        self._protected: set[int] = set()
-        # Set by the scheduler while the head waiting request cannot be admitted.
+        # Set by the scheduler while the head of the waiting queue cannot be admitted.
         self.admission_blocked = False
+        self._release_gen = 0
+        self._last_prefetch = None  # (request, free blocks) of the last prefetch attempt
+        # Idle hits a waiting request's prefetch keeps for it; MRU recycling skips them.
+        self._protected: set[int] = set()
+
+    @property
+    def free_block_ids(self) -> FreeOrder:
+        return self._free
+
+    @free_block_ids.setter
+    def free_block_ids(self, ids: Iterable[int]):
+        self._free = FreeOrder(ids)
 
     @classmethod
     def compute_hash(cls, token_ids: list[int], prefix: int = -1) -> int:
-        """xxh64 of the previous block's hash (8 bytes LE) then the int64 token ids (:67-73)."""
-        h = xxhash.xxh64()
-        if prefix != -1:
-            h.update(prefix.to_bytes(8, "little"))
-        h.update(np.array(token_ids).tobytes())
-        return h.intdigest()
+        """Chained block hash: xxh64 of the previous block's hash (8 bytes, little-endian; omitted for the
+        first block) followed by the int64 token ids (block_manager.py:67-73). CPU entries are keyed by it."""
+        head = b"" if prefix == -1 else prefix.to_bytes(8, "little")
+        return xxhash.xxh64_intdigest(head + np.asarray(token_ids, dtype=np.int64).tobytes())
 
-    def _is_published(self, block: Block) -> bool:
+    # -- block states ---------------------------------------------------------
+
+    def _published(self, block: Block) -> bool:
         return block.hash != -1 and self.hash_to_block_id.get(block.hash) == block.block_id
 
     def _victim(self) -> int:
-        """Next free block to recycle (:78-95): the oldest for LRU; for MRU
-        unpublished blocks first, then the latest release's blocks, tail first."""
+        """The free block to recycle next.
+
+        LRU: the front of the free order. MRU: the first block no prefix can
+        hit again; otherwise, among blocks a prefetch does not keep, the one
+        released last (highest release generation, then highest position in
+        its request), so the agent that finished last, and will likely return
+        last, loses its context first.
+        """
         if self.eviction == "lru":
-            return self.free_block_ids[0]
-        best_key, best_id = None, None
-        for block_id in self.free_block_ids:
+            return self._free[0]
+        best, best_rank = None, None
+        for block_id in self._free:
             block = self.blocks[block_id]
-            if not self._is_published(block):
+            if not self._published(block):
                 return block_id
             if block_id in self._protected:
                 continue
-            key = (block.release_gen, block.seq_index)
-            if best_key is None or key > best_key:
-                best_key, best_id = key, block_id
-        return best_id if best_id is not None else self.free_block_ids[0]
+            rank = (block.release_gen, block.seq_index)
+            if best_rank is None or rank > best_rank:
+                best, best_rank = block_id, rank
+        return self._free[0] if best is None else best
 
     def _allocate_block(self, order_writes: bool = True) -> int:
-        """Recycle a free block (:97-116). A published victim is saved to the
-        CPU tier before its hash is dropped; a save failure leaves it free and
-        indexed. order_writes makes the caller's stream wait for pending copies."""
+        """Recycle a free block for a new owner and return its id.
+
+        A published victim is offered to the CPU tier first; if that raises,
+        nothing has changed (the block stays free and published). With
+        order_writes, later writes on the caller's stream wait for copies
+        still reading or writing the block; a restore into the block orders
+        itself instead.
+        """
         block_id = self._victim()
         block = self.blocks[block_id]
-        assert block.ref_count == 0
-        if self._is_published(block):
-            if self._cpu_prefix_cache is not None:
-                self._cpu_prefix_cache._preserve_before_recycle(block.hash)
+        assert block.ref_count == 0, f"free block {block_id} is referenced"
+        tier = self._cpu_prefix_cache
+        if self._published(block):
+            if tier is not None:
+                tier._preserve_before_recycle(block.hash)
             del self.hash_to_block_id[block.hash]
-        if order_writes and self._cpu_prefix_cache is not None:
-            self._cpu_prefix_cache.before_block_reuse(block_id)
-        if self.free_block_ids[0] == block_id:
-            self.free_block_ids.popleft()
-        else:
-            self.free_block_ids.remove(block_id)
+        if order_writes and tier is not None:
+            tier.before_block_reuse(block_id)
+        self._free.remove(block_id)
         self._protected.discard(block_id)
         block.reset()
         self.used_block_ids.add(block_id)
         return block_id
 
     def _deallocate_block(self, block_id: int):
-        """Return a block to the free list; an idle published block may be saved now (:118-127)."""
+        """Back to the free order (at the back); a published block may be saved now."""
         block = self.blocks[block_id]
-        assert block.ref_count == 0
+        assert block.ref_count == 0, f"block {block_id} is still referenced"
         self.used_block_ids.remove(block_id)
-        self.free_block_ids.append(block_id)
-        if self._cpu_prefix_cache is not None and self._is_published(block):
-            self._cpu_prefix_cache._preserve_on_release(block.hash)
+        self._free.append(block_id)
+        tier = self._cpu_prefix_cache
+        if tier is not None and self._published(block):
+            tier._preserve_on_release(block.hash)
 
     def _acquire_block(self, block_id: int):
-        """Take a reference on a GPU hit; readers wait for a pending restore into it (:129-137)."""
+        """A reference on a GPU hit. Readers wait for any restore still copying into it (also when shared:
+        another request's split span may be copying it)."""
         block = self.blocks[block_id]
         if block.ref_count == 0:
-            self.free_block_ids.remove(block_id)
+            self._free.remove(block_id)
             self.used_block_ids.add(block_id)
         if self._cpu_prefix_cache is not None:
             self._cpu_prefix_cache.before_block_use(block_id)
@@ -155,248 +295,265 @@ class BlockManager:
         if block.ref_count == 0:
             self._deallocate_block(block_id)
 
-    def restore_cached_block(self, prefix_hash: int, token_ids: TokenSequence[int],
-                             copy_to_block: Callable[[int], None]) -> int:
-        """Reserve, populate, then publish one full idle prefix block (:145-183).
-
-        An existing GPU hit is returned without copying. On copy failure the
-        destination returns to the free list unpublished and the error
-        propagates; an idle victim it recycled stays evicted.
-        """
-        tokens = list(token_ids)
-        if (type(prefix_hash) is not int or not 0 <= prefix_hash < 2**64
-                or len(tokens) != self.block_size):
-            raise ValueError("restore requires a valid prefix hash and one full block")
-        existing = self.hash_to_block_id.get(prefix_hash)
-        if existing is not None:
-            block = self.blocks[existing]
-            if block.hash != prefix_hash or block.token_ids != tokens:
-                raise ValueError("prefix hash has conflicting token metadata")
-            return existing
-        if not self.free_block_ids:
-            raise MemoryError("not enough free KV blocks to restore a prefix")
-        block_id = self._allocate_block(order_writes=False)
-        block = self.blocks[block_id]
-        try:
-            copy_to_block(block_id)
-            block.update(prefix_hash, tokens)
-            self.hash_to_block_id[prefix_hash] = block_id
-        except BaseException:
-            if self.hash_to_block_id.get(prefix_hash) == block_id:
-                del self.hash_to_block_id[prefix_hash]
-            block.hash, block.token_ids = -1, []
-            raise
-        finally:
-            block.ref_count = 0
-            self._deallocate_block(block_id)
-        return block_id
-
-    def _full_block_hashes(self, seq: Sequence, count: int):
-        """Memoised (chained hash, token list, token tuple) of a sequence's leading blocks (:185-200)."""
-        memo = getattr(seq, "_block_hash_memo", None)
-        if memo is None:
-            memo = seq._block_hash_memo = []
-        h = memo[-1][0] if memo else -1
-        for i in range(len(memo), count):
-            token_ids = seq.block(i)
-            h = self.compute_hash(token_ids, h)
-            memo.append((h, token_ids, tuple(token_ids)))
-        return memo
-
-    def _batched_copies(self):
-        """The cache's coalesce() context (restores handed over as batches), if it has one."""
+    def _batched(self):
+        """The tier's coalesce() context, if it has one (copies are then issued as batches)."""
         coalesce = getattr(self._cpu_prefix_cache, "coalesce", None)
         return coalesce() if coalesce is not None else nullcontext()
 
-    def prefetch(self, seq: Sequence, reserve: int = 0) -> int:
-        """Start background restores of a waiting request's CPU hits (:202-237); returns how many.
+    # -- prefix lookup --------------------------------------------------------
 
-        Uses only free blocks beyond `reserve` and this request's own idle
-        hits, never recycling the latter. Throttled while nothing changed.
+    def _block_hashes(self, seq: Sequence, count: int):
+        """(hash, token list, token tuple) of the request's first `count` full blocks, cached on the request."""
+        known = seq.block_hashes
+        prev = known[-1][0] if known else -1
+        while len(known) < count:
+            tokens = seq.block(len(known))
+            prev = self.compute_hash(tokens, prev)
+            known.append((prev, tokens, tuple(tokens)))
+        return known
+
+    def _prefix_hits(self, seq: Sequence) -> list[PrefixHit]:
+        """The request's leading full blocks found on the GPU or in the CPU tier, up to the first miss.
+
+        The last block is never a hit (its last token must be computed), so
+        at most num_blocks - 1. Pure lookup: nothing is copied or changed.
         """
-        cache = self._cpu_prefix_cache
-        if cache is None or not cache.prefetch_enabled:
-            return 0
-        key = (seq.seq_id, len(self.free_block_ids))
-        if key == self._last_prefetch:
-            return 0
-        self._last_prefetch = key
-        prefix = self._prefix_blocks(seq)
-        own_idle = [block_id for _, _, block_id, _ in prefix
-                    if block_id is not None and self.blocks[block_id].ref_count == 0]
-        budget = len(self.free_block_ids) - reserve - len(own_idle)
-        if budget <= 0 or all(entry is None for *_, entry in prefix):
-            return 0
-        # Recycle other idle blocks first: this request's hits go to the back.
-        for block_id in own_idle:
-            self.free_block_ids.remove(block_id)
-            self.free_block_ids.append(block_id)
-        self._protected = set(own_idle)
-        started = 0
-        with self._batched_copies():
-            for h, token_ids, block_id, entry in prefix:
-                if started == budget:
-                    break
-                if entry is None:
-                    continue
-                target = self.restore_cached_block(
-                    h, token_ids, lambda target, e=entry: cache._copy_entry(e, target, wait=False))
-                self._protected.add(target)
-                started += 1
-        cache._prefetched_blocks += started
-        return started
-
-    def _prefix_blocks(self, seq: Sequence):
-        """Leading contiguous GPU hits (block id) and CPU hits (entry); pure lookup (:239-256)."""
-        prefix = []
-        memo = self._full_block_hashes(seq, seq.num_blocks - 1)
-        for i in range(seq.num_blocks - 1):
-            h, token_ids, token_tuple = memo[i]
+        hits = []
+        tier = self._cpu_prefix_cache
+        for i, (h, tokens, key) in enumerate(self._block_hashes(seq, seq.num_blocks - 1)):
             block_id = self.hash_to_block_id.get(h)
             if block_id is not None:
                 block = self.blocks[block_id]
-                if block.hash != h or block.token_ids != token_ids:
-                    break
-                prefix.append((h, token_ids, block_id, None))
+                if block.hash != h or block.token_ids != tokens:
+                    break  # a hash collision: treat as a miss
+                hits.append(PrefixHit(i, h, tokens, block_id, None))
                 continue
-            cache = self._cpu_prefix_cache
-            entry = cache._entry_for(h, token_tuple) if cache is not None else None
+            entry = tier._entry_for(h, key) if tier is not None else None
             if entry is None:
                 break
-            prefix.append((h, token_ids, None, entry))
-        return prefix
+            hits.append(PrefixHit(i, h, tokens, None, entry))
+        return hits
 
-    def _blocks_needed(self, seq: Sequence, prefix) -> int:
-        return seq.num_blocks - sum(block_id in self.used_block_ids for _, _, block_id, _ in prefix)
+    def _new_blocks_needed(self, seq: Sequence, hits: list[PrefixHit]) -> int:
+        """Free blocks an admission consumes: all but the hits other requests already reference."""
+        shared = sum(1 for hit in hits if hit.block_id is not None and hit.block_id in self.used_block_ids)
+        return seq.num_blocks - shared
+
+    def _split_point(self, hits: list[PrefixHit]) -> int:
+        """Leading CPU hits to recompute under the tier's hybrid costs (0: restore every CPU hit).
+
+        Only the CPU-only run before the first GPU hit can be split; a split
+        that reaches that GPU hit restores nothing and so does not pay.
+        """
+        tier = self._cpu_prefix_cache
+        if tier is None or tier.hybrid is None:
+            return 0
+        lead = next((hit.index for hit in hits if hit.block_id is not None), len(hits))
+        k = plan_split(lead, self.block_size, *tier.hybrid)
+        return k if k < lead or lead == len(hits) else 0
+
+    # -- admission --------------------------------------------------------------
 
     def can_allocate(self, seq: Sequence) -> int:
-        """Number of leading cached blocks, or -1 if the request cannot fit now (:258-264)."""
-        prefix = self._prefix_blocks(seq)
-        if len(self.free_block_ids) < self._blocks_needed(seq, prefix):
-            return -1
-        return len(prefix)
+        """Leading cached blocks the request can reuse, or -1 if it cannot be admitted now."""
+        hits = self._prefix_hits(seq)
+        return -1 if len(self._free) < self._new_blocks_needed(seq, hits) else len(hits)
 
     def allocate(self, seq: Sequence, num_cached_blocks: int):
-        """Admit a request with its first num_cached_blocks cached (:266-316).
+        """Give the request its block table, reusing its first `num_cached_blocks` cached blocks.
 
-        GPU hits are referenced first so no restore or allocation can recycle
-        them; CPU hits are restored (all of them, or only the tail after a
-        hybrid split whose head is recomputed); the rest are fresh blocks.
-        Any failure releases everything this call took.
+        GPU hits are referenced first, so no recycling below can take them.
+        CPU hits are restored into recycled blocks and published, waited for
+        on the caller's stream unless a hybrid split recomputes the head (the
+        restored span is then pending until finish_restore_span). The other
+        blocks are fresh. On any failure every reference taken is dropped and
+        the error propagates.
         """
-        assert not seq.block_table
-        prefix = self._prefix_blocks(seq)
-        if not 0 <= num_cached_blocks <= len(prefix):
+        assert not seq.block_table, "request already has blocks"
+        hits = self._prefix_hits(seq)
+        if not 0 <= num_cached_blocks <= len(hits):
             raise ValueError("requested prefix is no longer available")
-        prefix = prefix[:num_cached_blocks]
-        if len(self.free_block_ids) < self._blocks_needed(seq, prefix):
+        hits = hits[:num_cached_blocks]
+        if len(self._free) < self._new_blocks_needed(seq, hits):
             raise MemoryError("not enough free KV blocks to admit the request")
-        split = self._plan_split(prefix)
-        if split == len(prefix):
-            prefix, num_cached_blocks, split = [], 0, 0  # Recomputing everything is fastest.
+        split = self._split_point(hits)
+        if split == len(hits):  # recomputing the whole prefix is cheapest
+            hits, split = [], 0
+        tier = self._cpu_prefix_cache
         self._protected.clear()
         table = [-1] * seq.num_blocks
-        owned = []
-        try:
-            for i, (_, _, block_id, _) in enumerate(prefix):
-                if block_id is not None:
-                    self._acquire_block(block_id)
-                    owned.append(block_id)
-                    table[i] = block_id
-            with self._batched_copies():
-                for i, (h, token_ids, block_id, entry) in enumerate(prefix):
-                    if block_id is not None or i < split:
+        with _Taken(self) as taken:
+            for hit in hits:
+                if hit.block_id is not None:
+                    self._acquire_block(hit.block_id)
+                    taken.ids.append(hit.block_id)
+                    table[hit.index] = hit.block_id
+            with self._batched():
+                for hit in hits:
+                    if hit.block_id is not None or hit.index < split:
                         continue
                     block_id = self._allocate_block()
-                    owned.append(block_id)
-                    table[i] = block_id
-                    # After a split, the head's prefill overlaps these copies and
-                    # finish_restore_span orders the first read after them.
+                    taken.ids.append(block_id)
+                    table[hit.index] = block_id
                     if split:
-                        self._cpu_prefix_cache._copy_entry(entry, block_id, wait=False)
+                        tier._copy_entry(hit.entry, block_id, wait=False)
                     else:
-                        self._cpu_prefix_cache._copy_entry(entry, block_id)
-                    self.blocks[block_id].update(h, token_ids)
-                    self.hash_to_block_id[h] = block_id
-                for i in [*range(split), *range(num_cached_blocks, seq.num_blocks)]:
+                        tier._copy_entry(hit.entry, block_id)
+                    self.blocks[block_id].update(hit.hash, hit.tokens)
+                    self.hash_to_block_id[hit.hash] = block_id
+                for i in [*range(split), *range(len(hits), seq.num_blocks)]:
                     block_id = self._allocate_block()
-                    owned.append(block_id)
+                    taken.ids.append(block_id)
                     table[i] = block_id
-        except BaseException:
-            for block_id in reversed(owned):
-                self._release_block(block_id)
-            raise
         seq.block_table = table
         if split:
             seq.num_cached_tokens = 0
-            seq.restore_span = (split * self.block_size, num_cached_blocks * self.block_size)
+            seq.restore_span = (split * self.block_size, len(hits) * self.block_size)
         else:
-            seq.num_cached_tokens = num_cached_blocks * self.block_size
-
-    def _plan_split(self, prefix) -> int:
-        """Leading CPU-only blocks to recompute (0: restore every hit) (:318-327)."""
-        cache = self._cpu_prefix_cache
-        if cache is None or cache.hybrid is None:
-            return 0
-        lead = next((i for i, (_, _, block_id, _) in enumerate(prefix) if block_id is not None), len(prefix))
-        split = plan_split(lead, self.block_size, *cache.hybrid)
-        # Splitting before a GPU hit only helps if something still restores.
-        return split if split < lead or lead == len(prefix) else 0
+            seq.num_cached_tokens = len(hits) * self.block_size
 
     def finish_restore_span(self, seq: Sequence):
-        """Skip a split admission's restored span once its head is prefilled (:329-336)."""
+        """The head of a split admission is prefilled: skip the restored span; its first reads wait for it."""
         start, end = seq.restore_span
-        assert seq.num_cached_tokens == start
+        assert seq.num_cached_tokens == start, "the head is not prefilled yet"
         seq.restore_span = None
         seq.num_cached_tokens = end
         for block_id in seq.block_table[start // self.block_size:end // self.block_size]:
             self._cpu_prefix_cache.before_block_use(block_id)
 
     def deallocate(self, seq: Sequence):
-        """Release a request's blocks tail first, stamping MRU order (:338-347)."""
+        """Release the request's blocks, last block first, stamping their MRU rank."""
         self._release_gen += 1
-        for i, block_id in enumerate(seq.block_table):
-            self.blocks[block_id].release_gen = self._release_gen
-            self.blocks[block_id].seq_index = i
-        with self._batched_copies():
+        for position, block_id in enumerate(seq.block_table):
+            block = self.blocks[block_id]
+            block.release_gen, block.seq_index = self._release_gen, position
+        with self._batched():
             for block_id in reversed(seq.block_table):
                 self._release_block(block_id)
+        seq.block_table.clear()
         seq.num_cached_tokens = 0
         seq.restore_span = None
-        seq.block_table.clear()
 
     def allocate_for_resume(self, seq: Sequence, num_cached_tokens: int):
-        """Fresh blocks for imported KV, leaving the pending token to decode (:349-367)."""
+        """Fresh blocks for a request whose KV is copied in (KV handoff); the one uncached token decodes next.
+
+        A pending token at a block boundary gets its block from may_append on
+        that decode step, not here. Blocks are published after their copy.
+        """
         if seq.block_table or not 0 < num_cached_tokens == len(seq) - 1:
             raise ValueError("resume needs an empty block table and one uncached token")
-        num_blocks = -(-num_cached_tokens // self.block_size)
-        if len(self.free_block_ids) < num_blocks:
+        needed = -(-num_cached_tokens // self.block_size)
+        if len(self._free) < needed:
             raise MemoryError("not enough free KV blocks to resume")
         try:
-            for _ in range(num_blocks):
+            while len(seq.block_table) < needed:
                 seq.block_table.append(self._allocate_block())
         except BaseException:
             self.deallocate(seq)
             raise
         seq.num_cached_tokens = num_cached_tokens
 
+    # -- decode growth and publication -------------------------------------------
+
     def can_append(self, seq: Sequence) -> bool:
-        return len(self.free_block_ids) >= (len(seq) % self.block_size == 1)
+        """Whether the next decode step's token has a block (one is needed when it opens a new block)."""
+        opens_block = len(seq) % self.block_size == 1
+        return len(self._free) >= int(opens_block)
 
     def may_append(self, seq: Sequence):
         if len(seq) % self.block_size == 1:
             seq.block_table.append(self._allocate_block())
 
     def hash_blocks(self, seq: Sequence):
-        """Publish the chained hashes of blocks this step completed (:376-386)."""
-        start = seq.num_cached_tokens // self.block_size
-        end = (seq.num_cached_tokens + seq.num_scheduled_tokens) // self.block_size
-        if start == end:
+        """Publish the blocks this step fills (tokens [num_cached, num_cached + num_scheduled))."""
+        first = seq.num_cached_tokens // self.block_size
+        stop = (seq.num_cached_tokens + seq.num_scheduled_tokens) // self.block_size
+        if first == stop:
             return
-        h = self.blocks[seq.block_table[start - 1]].hash if start > 0 else -1
-        for i in range(start, end):
+        prev = self.blocks[seq.block_table[first - 1]].hash if first else -1
+        for i in range(first, stop):
+            tokens = seq.block(i)
+            prev = self.compute_hash(tokens, prev)
             block = self.blocks[seq.block_table[i]]
-            token_ids = seq.block(i)
-            h = self.compute_hash(token_ids, h)
-            block.update(h, token_ids)
-            self.hash_to_block_id[h] = block.block_id
+            block.update(prev, tokens)
+            self.hash_to_block_id[prev] = block.block_id
+
+    # -- restores outside admission --------------------------------------------------
+
+    def restore_cached_block(self, prefix_hash: int, token_ids: TokenSequence[int],
+                             copy_to_block: Callable[[int], None]) -> int:
+        """Copy one full prefix block into an idle GPU block and publish it; returns its id.
+
+        An existing GPU hit is returned without a copy. The destination is
+        recycled without write ordering: `copy_to_block` must order its copy
+        after pending work itself and make later readers wait (the CPU tier's
+        restore stream does both). If the copy raises, the destination goes
+        back to the free order unpublished and the error propagates (an idle
+        victim it recycled stays evicted). Call between steps.
+        """
+        tokens = list(token_ids)
+        if type(prefix_hash) is not int or not 0 <= prefix_hash < _HASH_LIMIT or len(tokens) != self.block_size:
+            raise ValueError("restore requires a valid prefix hash and one full block")
+        known = self.hash_to_block_id.get(prefix_hash)
+        if known is not None:
+            block = self.blocks[known]
+            if block.hash != prefix_hash or block.token_ids != tokens:
+                raise ValueError("prefix hash has conflicting token metadata")
+            return known
+        if not self._free:
+            raise MemoryError("not enough free KV blocks to restore a prefix")
+        block_id = self._allocate_block(order_writes=False)
+        block = self.blocks[block_id]
+        published = False
+        try:
+            copy_to_block(block_id)
+            block.update(prefix_hash, tokens)
+            self.hash_to_block_id[prefix_hash] = block_id
+            published = True
+        finally:
+            if not published:
+                if self.hash_to_block_id.get(prefix_hash) == block_id:
+                    del self.hash_to_block_id[prefix_hash]
+                block.update(-1, [])
+            block.ref_count = 0
+            self._deallocate_block(block_id)
+        return block_id
+
+    def prefetch(self, seq: Sequence, reserve: int = 0) -> int:
+        """Start background restores of a waiting request's CPU hits; returns how many were started.
+
+        Restored blocks become idle GPU hits, so the admission skips their
+        copies. Uses only free blocks beyond `reserve` (kept for running
+        requests' growth) and never recycles the request's own idle GPU hits,
+        which move to the back of the free order and are kept from MRU
+        recycling. Needs a tier with prefetch_enabled; does nothing when
+        called again with the same request and free-block count. Call
+        between steps.
+        """
+        tier = self._cpu_prefix_cache
+        if tier is None or not tier.prefetch_enabled:
+            return 0
+        attempt = (seq.seq_id, len(self._free))
+        if attempt == self._last_prefetch:
+            return 0
+        self._last_prefetch = attempt
+        hits = self._prefix_hits(seq)
+        own_idle = [hit.block_id for hit in hits
+                    if hit.block_id is not None and self.blocks[hit.block_id].ref_count == 0]
+        budget = len(self._free) - reserve - len(own_idle)
+        cpu_hits = [hit for hit in hits if hit.entry is not None]
+        if budget <= 0 or not cpu_hits:
+            return 0
+        for block_id in own_idle:
+            self._free.move_to_back(block_id)
+        self._protected = set(own_idle)
+        started = 0
+        with self._batched():
+            for hit in cpu_hits[:budget]:
+                target = self.restore_cached_block(
+                    hit.hash, hit.tokens, lambda block_id, entry=hit.entry: tier._copy_entry(entry, block_id,
+                                                                                             wait=False))
+                self._protected.add(target)
+                started += 1
+        tier._prefetched_blocks += started
+        return started

@@ -1,11 +1,22 @@
-"""Uncompressed KV handoff of a running request between engines (TP=1).
+"""KV handoff: move a running request, with its KV, from one engine to another (TP=1).
 
-Same snapshot format and semantics as nanovllm/engine/kv_handoff.py: the
-payload holds the written tokens only, in logical order, on the CPU, as
-[K/V, layer, token, KV head, head dim]. The gather (export) and scatter
-(import) run as libkvx token-copy kernels instead of index_select + per-block
-copy_; the payload lives in pinned host memory, which the kernels read and
-write across the host link directly.
+A KVSnapshot holds a request's tokens and sampling limits and the KV of
+every token but the pending last one, in logical token order, in pinned host
+memory. Two payload formats:
+
+- BF16 (the reference's, nanovllm/engine/kv_handoff.py:17-59): `kv` is
+  [2, L, T, H, hd] in the pool dtype; import reproduces the pool bytes exactly.
+- FP8: `kv` is float8_e4m3fn [2, L, T, H, hd] and `scale` [2, L, T, H, 1]
+  (bfloat16 or float32): exactly fp8_quantize of the BF16 payload
+  (nanovllm/engine/cpu_prefix_cache.py:20-24), 0.51-0.52x its bytes.
+  Import writes fp8_dequantize of it, as a restore from the CPU tier does.
+
+Export runs one token-gather kernel per 128 blocks that writes the pinned
+payload across the host link itself (quantising on the way for FP8) and
+waits for it. Import copies the payload into device memory with one DMA per
+tensor, then scatters it (dequantising for FP8) into freshly allocated
+blocks; it returns after those copies finish, so the caller may free or
+reuse the snapshot immediately.
 """
 
 from dataclasses import dataclass
@@ -13,7 +24,6 @@ from dataclasses import dataclass
 import torch
 
 from kvx import ops
-from kvx.engine.handoff_timing import PhaseTimer
 from kvx.engine.sequence import SamplingParams, Sequence, SequenceStatus
 
 
@@ -26,115 +36,124 @@ class KVSnapshot:
     temperature: float
     max_tokens: int
     ignore_eos: bool
-    kv: torch.Tensor  # [K/V, layer, written token, KV head, head dim], CPU
+    kv: torch.Tensor  # [K/V, layer, token, KV head, head dim], pinned host memory
+    scale: torch.Tensor | None = None  # FP8 only: [K/V, layer, token, KV head, 1]
 
     @property
-    def payload_bytes(self):
-        return self.kv.numel() * self.kv.element_size()
+    def fp8(self) -> bool:
+        return self.kv.dtype == torch.float8_e4m3fn
+
+    @property
+    def payload_bytes(self) -> int:
+        total = self.kv.numel() * self.kv.element_size()
+        if self.scale is not None:
+            total += self.scale.numel() * self.scale.element_size()
+        return total
 
 
-def export_kv(runner, seq: Sequence) -> KVSnapshot:
-    """Snapshot a running request between steps (kv_handoff.py:34-59).
-
-    Timed phases (handoff_timing): gather_blocks allocates the pinned payload,
-    pack queues the gather kernel that packs the blocks' written tokens into
-    it, and copy_to_host waits for that kernel, whose writes cross the host link.
-    """
+def _require_tp1(runner):
     if runner.world_size != 1:
         raise NotImplementedError("KV handoff currently requires tensor_parallel_size=1")
-    if seq.status != SequenceStatus.RUNNING or seq.num_scheduled_tokens:
+
+
+def export_kv(runner, seq: Sequence, *, fp8: bool = False, scale_dtype: torch.dtype = torch.float32) -> KVSnapshot:
+    """Snapshot a running request between steps (kv_handoff.py:34-59); fp8=True sends FP8 codes and scales."""
+    _require_tp1(runner)
+    if seq.status is not SequenceStatus.RUNNING or seq.num_scheduled_tokens:
         raise ValueError("export requires a running sequence between steps")
     count = seq.num_cached_tokens
     if count <= 0 or count != len(seq) - 1:
         raise ValueError("export requires exactly one pending, uncached token")
-    num_blocks = -(-count // runner.block_size)
-    timer = PhaseTimer("export_kv", seq_id=seq.seq_id, num_tokens=count, num_blocks=num_blocks)
+    blocks = -(-count // runner.block_size)
+    if len(seq.block_table) < blocks:
+        raise ValueError("sequence is missing KV blocks")
     pool = runner.kv_cache
-    with timer.phase("gather_blocks"):
-        if len(seq.block_table) < num_blocks:
-            raise ValueError("sequence is missing KV blocks")
-        # The gather kernel writes the pinned host payload itself (one pass over the
-        # host link, 54 GB/s on MI355X for a 32K-token Qwen3-8B request, against
-        # 4.1 GB/s for a device gather followed by a pageable .cpu() copy).
-        payload = torch.empty((2, pool.shape[1], count, *pool.shape[-2:]), dtype=pool.dtype, pin_memory=True)
-    with timer.phase("pack"):
-        ops.gather_tokens(pool, seq.block_table[:num_blocks], count, payload)
-    with timer.phase("copy_to_host"):
-        torch.cuda.current_stream(pool.device).synchronize()
-    timer.finish(payload_bytes=payload.numel() * payload.element_size())
-    return KVSnapshot(seq.token_ids.copy(), seq.num_prompt_tokens, count, runner.block_size, seq.temperature,
-                      seq.max_tokens, seq.ignore_eos, payload)
+    shape = (2, pool.shape[1], count, *pool.shape[-2:])
+    table = seq.block_table[:blocks]
+    scale = None
+    if fp8:
+        if scale_dtype not in ops.SCALE_DTYPES:
+            raise ValueError("FP8 scales must be bfloat16 or float32")
+        kv = torch.empty(shape, dtype=torch.float8_e4m3fn, pin_memory=True)
+        scale = torch.empty((*shape[:-1], 1), dtype=scale_dtype, pin_memory=True)
+        ops.gather_tokens_fp8(pool, table, count, kv, scale)
+    else:
+        kv = torch.empty(shape, dtype=pool.dtype, pin_memory=True)
+        ops.gather_tokens(pool, table, count, kv)
+    torch.cuda.current_stream(pool.device).synchronize()
+    return KVSnapshot(list(seq.token_ids), seq.num_prompt_tokens, count, runner.block_size, seq.temperature,
+                      seq.max_tokens, seq.ignore_eos, kv, scale)
 
 
-def verify_imported_kv(runner, seq: Sequence, snapshot: KVSnapshot) -> bool:
-    """Byte-compare the imported blocks with the snapshot, one block at a time (kv_handoff.py:62-77)."""
+def _check_snapshot(runner, block_manager, snapshot: KVSnapshot):
     pool = runner.kv_cache
-    for logical, physical in enumerate(seq.block_table):
-        start = logical * runner.block_size
-        end = min(start + runner.block_size, snapshot.num_cached_tokens)
-        if end <= start:
-            break
-        actual = pool[:, :, physical, :end - start].cpu()
-        expected = snapshot.kv[:, :, start:end]
-        if not torch.equal(actual.view(torch.uint8), expected.contiguous().view(torch.uint8)):
-            return False
-    return True
+    shape = (2, pool.shape[1], snapshot.num_cached_tokens, *pool.shape[-2:])
+    if snapshot.fp8:
+        payload_ok = (snapshot.scale is not None and tuple(snapshot.scale.shape) == (*shape[:-1], 1)
+                      and snapshot.scale.dtype in ops.SCALE_DTYPES and snapshot.scale.device.type == "cpu")
+    else:
+        payload_ok = snapshot.kv.dtype == pool.dtype and snapshot.scale is None
+    if (not payload_ok or snapshot.block_size != runner.block_size or block_manager.block_size != runner.block_size
+            or tuple(snapshot.kv.shape) != shape or snapshot.kv.device.type != "cpu"):
+        raise ValueError("snapshot layout, dtype or block size does not match this worker")
+    tokens = len(snapshot.token_ids)
+    if (not 0 < snapshot.num_prompt_tokens < tokens or snapshot.num_cached_tokens != tokens - 1
+            or tokens - snapshot.num_prompt_tokens >= snapshot.max_tokens):
+        raise ValueError("snapshot must contain an unfinished completion and one uncached token")
+
+
+def _to_device(t: torch.Tensor, device: torch.device) -> torch.Tensor:
+    return t.contiguous().to(device, non_blocking=t.is_pinned())
 
 
 def import_kv(runner, block_manager, snapshot: KVSnapshot) -> Sequence:
-    """Allocate fresh blocks and rebuild a decode-ready sequence (kv_handoff.py:80-135).
+    """Allocate fresh blocks, copy the snapshot's KV into them and return a decode-ready request (:80-135).
 
-    Failure after allocation releases the blocks; prefix hashes are published
-    only after the scatter is queued. Timed phases (handoff_timing) as the
-    reference's; copy_to_device only copies a payload that is not pinned (a
-    pinned one is read in place by the scatter kernel, queued in scatter_blocks).
+    The blocks' prefix hashes are published once the copies are queued; if
+    anything fails after allocation the blocks are released. Returns after
+    the copies completed (the snapshot is no longer read).
     """
-    if runner.world_size != 1:
-        raise NotImplementedError("KV handoff currently requires tensor_parallel_size=1")
-    timer = PhaseTimer("import_kv", num_cached_tokens=snapshot.num_cached_tokens,
-                       num_tokens=len(snapshot.token_ids))
-    seq = None
+    _require_tp1(runner)
+    _check_snapshot(runner, block_manager, snapshot)
+    params = SamplingParams(temperature=snapshot.temperature, max_tokens=snapshot.max_tokens,
+                            ignore_eos=snapshot.ignore_eos)
+    seq = Sequence.resumed(snapshot.token_ids, snapshot.num_prompt_tokens, params)
+    block_manager.allocate_for_resume(seq, snapshot.num_cached_tokens)
+    pool = runner.kv_cache
+    count = snapshot.num_cached_tokens
     try:
-        with timer.phase("validate"):
-            pool = runner.kv_cache
-            expected = (2, pool.shape[1], snapshot.num_cached_tokens, *pool.shape[-2:])
-            if (snapshot.block_size != runner.block_size or block_manager.block_size != runner.block_size
-                    or tuple(snapshot.kv.shape) != expected or snapshot.kv.dtype != pool.dtype
-                    or snapshot.kv.device.type != "cpu"):
-                raise ValueError("snapshot layout, dtype or block size does not match this worker")
-            if (not 0 < snapshot.num_prompt_tokens < len(snapshot.token_ids)
-                    or snapshot.num_cached_tokens != len(snapshot.token_ids) - 1
-                    or len(snapshot.token_ids) - snapshot.num_prompt_tokens >= snapshot.max_tokens):
-                raise ValueError("snapshot must contain an unfinished completion and one uncached token")
-        with timer.phase("rebuild_sequence"):
-            seq = Sequence(snapshot.token_ids[:snapshot.num_prompt_tokens],
-                           SamplingParams(temperature=snapshot.temperature, max_tokens=snapshot.max_tokens,
-                                          ignore_eos=snapshot.ignore_eos))
-            for token in snapshot.token_ids[snapshot.num_prompt_tokens:]:
-                seq.append_token(token)
-        with timer.phase("allocate_blocks"):
-            block_manager.allocate_for_resume(seq, snapshot.num_cached_tokens)
-        with timer.phase("copy_to_device"):
-            # A pinned payload (what export_kv produces) is read by the scatter kernel in place, so it must stay
-            # unchanged until the stream has run the scatter (resume_request synchronizes); others are copied first.
-            payload = snapshot.kv
-            if not (payload.is_pinned() and payload.is_contiguous()):
-                payload = payload.to(device=pool.device).contiguous()
-        with timer.phase("scatter_blocks"):
-            ops.scatter_tokens(pool, seq.block_table, snapshot.num_cached_tokens, payload)
-        with timer.phase("publish_cache"):
-            # Prefix metadata becomes valid only once the payload's copy is queued.
-            seq.num_cached_tokens = 0
-            seq.num_scheduled_tokens = snapshot.num_cached_tokens
-            block_manager.hash_blocks(seq)
-            seq.num_scheduled_tokens = 0
-            seq.num_cached_tokens = snapshot.num_cached_tokens
-            seq.status = SequenceStatus.RUNNING
-            seq.is_prefill = False
-        timer.finish(payload_bytes=lambda: snapshot.payload_bytes, num_blocks=lambda: len(seq.block_table))
-        return seq
-    except BaseException as error:
-        timer.abort(error)
-        if seq is not None:
-            block_manager.deallocate(seq)
+        kv = _to_device(snapshot.kv, pool.device)
+        if snapshot.fp8:
+            ops.scatter_tokens_fp8(pool, seq.block_table, count, kv, _to_device(snapshot.scale, pool.device))
+        else:
+            ops.scatter_tokens(pool, seq.block_table, count, kv)
+        seq.num_cached_tokens, seq.num_scheduled_tokens = 0, count
+        block_manager.hash_blocks(seq)
+        seq.num_cached_tokens, seq.num_scheduled_tokens = count, 0
+        seq.status = SequenceStatus.RUNNING
+        seq.is_prefill = False
+        torch.cuda.current_stream(pool.device).synchronize()
+    except BaseException:
+        block_manager.deallocate(seq)
         raise
+    return seq
+
+
+def verify_imported_kv(runner, seq: Sequence, snapshot: KVSnapshot) -> bool:
+    """Whether the request's blocks hold the snapshot's KV: its bytes (BF16) or their FP8 round trip (kv_handoff.py:62-77).
+
+    The comparison runs on the device: the request's tokens are gathered out
+    of its blocks and compared with the snapshot (dequantised for FP8).
+    """
+    pool = runner.kv_cache
+    count = snapshot.num_cached_tokens
+    if len(seq.block_table) < -(-count // runner.block_size):
+        return False
+    actual = torch.empty((2, pool.shape[1], count, *pool.shape[-2:]), dtype=pool.dtype, device=pool.device)
+    ops.gather_tokens(pool, seq.block_table, count, actual)
+    if snapshot.fp8:
+        expected = torch.empty_like(actual)
+        ops.fp8_dequantize(_to_device(snapshot.kv, pool.device), _to_device(snapshot.scale, pool.device), expected)
+    else:
+        expected = _to_device(snapshot.kv, pool.device)
+    return torch.equal(actual.view(torch.uint8), expected.view(torch.uint8))

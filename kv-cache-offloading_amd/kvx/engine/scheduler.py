@@ -1,54 +1,68 @@
-"""Continuous-batching scheduler: the caller that triggers saves, restores and prefetches.
+"""Continuous-batching scheduler: the caller whose admissions trigger restores, saves and prefetches.
 
-Behaviour follows nanovllm/engine/scheduler.py (line citations below): legacy
-or chunk-budgeted prefill policies, chunked prefill of the head request,
-split (hybrid) admissions whose head joins later requests, decode with
-preemption, and full rollback when a copy fails mid-batch. Admission blocking
-is what arms save-on-release and prefetch in the block manager.
+Each step is one homogeneous batch: prefill if any waiting request can be
+admitted, else decode; if decode preempted everything, prefill is tried
+once more (nanovllm/engine/scheduler.py:44-81, its default policy).
+
+Prefill admits waiting requests in order within a token budget. Only the
+first request of a batch may be chunked; a split (hybrid) admission
+schedules its head only, and requests behind it may join the batch while its
+restored span copies. A waiting request that does not fit sets
+`block_manager.admission_blocked` (which arms save-on-release in the CPU
+tier) and prefetches its CPU hits into spare blocks, keeping one block per
+running request for decode growth (:101-107).
+
+Decode gives each running request one token and a new block when it crosses
+a block boundary, preempting the newest running request (or itself) when no
+block is free.
+
+A failure anywhere in a prefill or decode pass (a copy that raises) undoes
+the whole pass: queues, request fields and the blocks the pass took are as
+before, so the step can be retried (:130-141, 172-180).
 """
 
 from collections import deque
-from dataclasses import dataclass
 
 from kvx.engine.block_manager import BlockManager
 from kvx.engine.sequence import Sequence, SequenceStatus
 
-PREFILL_POLICIES = ("legacy", "fixed", "decode_aware")
 
+class _PrefillUndo:
+    """What a prefill pass changed, for restoring it if the pass raises."""
 
-def validate_scheduling_options(policy, chunk_size, min_chunk_size, batch_tokens, batch_seqs):
-    """nanovllm/config.py:8-20."""
-    if policy not in PREFILL_POLICIES:
-        raise ValueError(f"prefill_policy must be one of {PREFILL_POLICIES}")
-    for name, value in (("prefill_chunk_size", chunk_size), ("prefill_min_chunk_size", min_chunk_size),
-                        ("max_num_batched_tokens", batch_tokens), ("max_num_seqs", batch_seqs)):
-        if type(value) is not int or value < 1:
-            raise ValueError(f"{name} must be a positive integer")
-    if min_chunk_size > chunk_size:
-        raise ValueError("prefill_min_chunk_size must not exceed prefill_chunk_size")
+    def __init__(self, scheduler: "Scheduler"):
+        self.scheduler = scheduler
+        self.waiting = list(scheduler.waiting)
+        self.touched: list[tuple[Sequence, int, int, SequenceStatus, bool]] = []
+        self.promoted: list[Sequence] = []
 
+    def note(self, seq: Sequence):
+        self.touched.append((seq, seq.num_cached_tokens, seq.num_scheduled_tokens, seq.status,
+                             bool(seq.block_table)))
 
-@dataclass(frozen=True)
-class ScheduleDecision:
-    policy: str
-    phase: str
-    prefill_budget: int
-    decode_requests: int  # runnable decoders before admission/preemption
-    scheduled_tokens: int
-    seq_ids: tuple[int, ...]
+    def restore(self):
+        manager = self.scheduler.block_manager
+        for seq, cached, scheduled, status, had_blocks in reversed(self.touched):
+            if seq.block_table and not had_blocks:
+                manager.deallocate(seq)
+            seq.num_cached_tokens, seq.num_scheduled_tokens, seq.status = cached, scheduled, status
+        for seq in self.promoted:
+            self.scheduler.running.remove(seq)
+        self.scheduler.waiting.clear()
+        self.scheduler.waiting.extend(self.waiting)
 
 
 class Scheduler:
+    """Queues and batching over one BlockManager.
+
+    `config` provides max_num_seqs, max_num_batched_tokens, eos,
+    kvcache_block_size, num_kvcache_blocks and optionally kv_eviction
+    ("lru" by default), as the reference's Config does.
+    """
 
     def __init__(self, config):
         self.max_num_seqs = config.max_num_seqs
         self.max_num_batched_tokens = config.max_num_batched_tokens
-        self.prefill_policy = getattr(config, "prefill_policy", "legacy")
-        self.prefill_chunk_size = getattr(config, "prefill_chunk_size", 512)
-        self.prefill_min_chunk_size = getattr(config, "prefill_min_chunk_size", 1)
-        validate_scheduling_options(self.prefill_policy, self.prefill_chunk_size, self.prefill_min_chunk_size,
-                                    self.max_num_batched_tokens, self.max_num_seqs)
-        self.last_schedule: ScheduleDecision | None = None
         self.eos = config.eos
         self.block_size = config.kvcache_block_size
         self.block_manager = BlockManager(config.num_kvcache_blocks, config.kvcache_block_size,
@@ -56,157 +70,119 @@ class Scheduler:
         self.waiting: deque[Sequence] = deque()
         self.running: deque[Sequence] = deque()
 
-    def is_finished(self):
+    def is_finished(self) -> bool:
         return not self.waiting and not self.running
 
     def add(self, seq: Sequence):
         self.waiting.append(seq)
 
-    def _decision(self, phase, budget, decode_requests, seqs):
-        self.last_schedule = ScheduleDecision(self.prefill_policy, phase, budget, decode_requests,
-                                              sum(seq.num_scheduled_tokens for seq in seqs),
-                                              tuple(seq.seq_id for seq in seqs))
-
     def schedule(self) -> tuple[list[Sequence], bool]:
-        """One homogeneous prefill or decode batch (scheduler.py:44-81).
-
-        Non-legacy policies cap prefill at a chunk budget and alternate
-        phases: after a prefill batch, runnable decoders go first.
-        """
-        decode_requests = len(self.running)
-        budget = self.max_num_batched_tokens
+        """The next batch and whether it is a prefill."""
         self.block_manager.admission_blocked = False
-        if self.prefill_policy != "legacy":
-            chunk = self.prefill_chunk_size
-            if self.prefill_policy == "decode_aware":
-                chunk = max(self.prefill_min_chunk_size, chunk // (1 + decode_requests))
-            budget = min(budget, chunk)
-        decode_due = (self.prefill_policy != "legacy" and self.running and self.last_schedule is not None
-                      and self.last_schedule.phase == "prefill")
-        for is_prefill in ((False, True) if decode_due else (True, False)):
-            seqs = self._schedule_prefill(budget) if is_prefill else self._schedule_decode()
-            if seqs:
-                self._decision("prefill" if is_prefill else "decode", budget, decode_requests, seqs)
-                return seqs, is_prefill
-        # Decode may have preempted everything, making a blocked prefill admissible.
-        seqs = self._schedule_prefill(budget)
-        if seqs:
-            self._decision("prefill", budget, decode_requests, seqs)
-            return seqs, True
+        for is_prefill, make in ((True, self._prefill_batch), (False, self._decode_batch),
+                                 (True, self._prefill_batch)):
+            batch = make()
+            if batch:
+                return batch, is_prefill
         raise RuntimeError("no request can progress: check GPU KV capacity and request lengths")
 
-    def _schedule_prefill(self, budget: int) -> list[Sequence]:
-        """Admit and chunk waiting requests (scheduler.py:83-143); a failure restores every request."""
-        scheduled: list[Sequence] = []
-        batched = 0
-        saved_state = []
-        removed = []
-        original_waiting = list(self.waiting)
-        i = 0  # requests before i are split admissions whose head is already scheduled
+    def _prefill_batch(self) -> list[Sequence]:
+        budget = self.max_num_batched_tokens
+        manager = self.block_manager
+        batch: list[Sequence] = []
+        used = 0
+        undo = _PrefillUndo(self)
         try:
-            while i < len(self.waiting) and len(scheduled) < self.max_num_seqs:
+            i = 0  # requests before i are split admissions whose head is already in this batch
+            while i < len(self.waiting) and len(batch) < self.max_num_seqs and used < budget:
                 seq = self.waiting[i]
-                remaining = budget - batched
-                if remaining == 0:
-                    break
-                saved_state.append((seq, seq.num_cached_tokens, seq.num_scheduled_tokens, seq.status,
-                                    bool(seq.block_table)))
-                if not seq.block_table:
-                    cached_blocks = self.block_manager.can_allocate(seq)
-                    if cached_blocks == -1:
-                        # Spend the wait restoring its CPU hits into spare blocks.
-                        self.block_manager.admission_blocked = True
-                        self.block_manager.prefetch(seq, reserve=len(self.running))
-                        break
-                    num_tokens = seq.num_tokens - cached_blocks * self.block_size
+                undo.note(seq)
+                cached_blocks = None
+                if seq.block_table:  # a chunked prefill, or a split head, continues
+                    new_tokens = seq.num_tokens - seq.num_cached_tokens
                 else:
-                    num_tokens = seq.num_tokens - seq.num_cached_tokens
-                if remaining < num_tokens and scheduled:  # only the first request may be chunked
+                    cached_blocks = manager.can_allocate(seq)
+                    if cached_blocks < 0:
+                        manager.admission_blocked = True
+                        manager.prefetch(seq, reserve=len(self.running))
+                        break
+                    new_tokens = seq.num_tokens - cached_blocks * self.block_size
+                room = budget - used
+                if batch and new_tokens > room:
                     break
-                if not seq.block_table:
-                    self.block_manager.allocate(seq, cached_blocks)
-                # A split admission prefills only up to its restore span first.
-                end = seq.restore_span[0] if seq.restore_span else seq.num_tokens
-                seq.num_scheduled_tokens = min(end - seq.num_cached_tokens, remaining)
-                batched += seq.num_scheduled_tokens
-                scheduled.append(seq)
-                if seq.num_cached_tokens + seq.num_scheduled_tokens == seq.num_tokens:
+                if cached_blocks is not None:
+                    manager.allocate(seq, cached_blocks)
+                stop = seq.restore_span[0] if seq.restore_span else seq.num_tokens
+                seq.num_scheduled_tokens = min(stop - seq.num_cached_tokens, room)
+                used += seq.num_scheduled_tokens
+                batch.append(seq)
+                reached = seq.num_cached_tokens + seq.num_scheduled_tokens
+                if reached == seq.num_tokens:
                     seq.status = SequenceStatus.RUNNING
                     del self.waiting[i]
-                    removed.append(seq)
+                    undo.promoted.append(seq)
                     self.running.append(seq)
-                elif seq.restore_span and seq.num_cached_tokens + seq.num_scheduled_tokens == seq.restore_span[0]:
-                    i += 1  # head fully scheduled; it stays queued while later requests join
+                elif seq.restore_span and reached == seq.restore_span[0]:
+                    i += 1
                 else:
-                    break  # a chunked prefill stays at the head of the queue
+                    break  # chunked: it stays at the head of the queue
         except BaseException:
-            for seq, cached, sched, status, had_blocks in reversed(saved_state):
-                if not had_blocks and seq.block_table:
-                    self.block_manager.deallocate(seq)
-                seq.num_cached_tokens, seq.num_scheduled_tokens, seq.status = cached, sched, status
-            for seq in removed:
-                self.running.remove(seq)
-            self.waiting.clear()
-            self.waiting.extend(original_waiting)
+            undo.restore()
             raise
-        return scheduled
+        return batch
 
-    def _schedule_decode(self) -> list[Sequence]:
-        """One token for each runnable request, preempting when blocks run out (scheduler.py:145-186)."""
-        scheduled: list[Sequence] = []
-        saved_state = []
+    def _decode_batch(self) -> list[Sequence]:
+        manager = self.block_manager
+        batch: list[Sequence] = []
+        before: list[tuple[Sequence, int, int, bool]] = []  # state of each request this pass grew
         try:
-            while self.running and len(scheduled) < self.max_num_seqs:
+            while self.running and len(batch) < self.max_num_seqs:
                 seq = self.running.popleft()
-                while not self.block_manager.can_append(seq):
-                    # Reclaim interleaved partial prefills before evicting live decoders.
-                    partial = next((item for item in reversed(self.waiting) if item.block_table), None)
-                    if self.prefill_policy != "legacy" and partial is not None:
-                        self.block_manager.deallocate(partial)
-                        continue
+                while seq is not None and not manager.can_append(seq):
                     if self.running:
                         self.preempt(self.running.pop())
                     else:
                         self.preempt(seq)
-                        break
-                else:
-                    saved_state.append((seq, len(seq.block_table), seq.num_scheduled_tokens, seq.is_prefill))
-                    seq.num_scheduled_tokens = 1
-                    seq.is_prefill = False
-                    self.block_manager.may_append(seq)
-                    scheduled.append(seq)
+                        seq = None
+                if seq is None:
+                    continue
+                before.append((seq, len(seq.block_table), seq.num_scheduled_tokens, seq.is_prefill))
+                seq.num_scheduled_tokens = 1
+                seq.is_prefill = False
+                manager.may_append(seq)
+                batch.append(seq)
         except BaseException:
-            for seq, old_length, sched, is_prefill in reversed(saved_state):
-                for block_id in reversed(seq.block_table[old_length:]):
-                    self.block_manager._release_block(block_id)
-                del seq.block_table[old_length:]
-                seq.num_scheduled_tokens, seq.is_prefill = sched, is_prefill
-            self.running.extendleft(reversed([seq for seq, *_ in saved_state]))
+            for seq, length, scheduled, was_prefill in reversed(before):
+                for block_id in reversed(seq.block_table[length:]):
+                    manager._release_block(block_id)
+                del seq.block_table[length:]
+                seq.num_scheduled_tokens, seq.is_prefill = scheduled, was_prefill
+            self.running.extendleft(reversed([seq for seq, *_ in before]))
             raise
-        if self.prefill_policy == "legacy":
-            self.running.extendleft(reversed(scheduled))
-        else:
-            self.running.extend(scheduled)  # more residents than batch slots all get decode time
-        return scheduled
+        self.running.extendleft(reversed(batch))
+        return batch
 
     def preempt(self, seq: Sequence):
+        """Back to the front of the waiting queue without its KV (it is recomputed or hit again)."""
         seq.status = SequenceStatus.WAITING
         seq.is_prefill = True
         self.block_manager.deallocate(seq)
         self.waiting.appendleft(seq)
 
     def postprocess(self, seqs: list[Sequence], token_ids: list[int], is_prefill: bool):
-        """Publish completed blocks, advance caches, append tokens, retire finished requests (:194-207)."""
+        """After the model ran: publish filled blocks, advance, append sampled tokens, retire finished requests."""
+        manager = self.block_manager
         for seq, token_id in zip(seqs, token_ids):
-            self.block_manager.hash_blocks(seq)
+            manager.hash_blocks(seq)
             seq.num_cached_tokens += seq.num_scheduled_tokens
             seq.num_scheduled_tokens = 0
             if seq.restore_span and seq.num_cached_tokens == seq.restore_span[0]:
-                self.block_manager.finish_restore_span(seq)
+                manager.finish_restore_span(seq)
             if is_prefill and seq.num_cached_tokens < seq.num_tokens:
-                continue
+                continue  # a chunk or a split head: no token is sampled yet
             seq.append_token(token_id)
-            if (not seq.ignore_eos and token_id == self.eos) or seq.num_completion_tokens == seq.max_tokens:
+            hit_eos = not seq.ignore_eos and token_id == self.eos
+            if hit_eos or seq.num_completion_tokens == seq.max_tokens:
                 seq.status = SequenceStatus.FINISHED
-                self.block_manager.deallocate(seq)
+                manager.deallocate(seq)
                 self.running.remove(seq)

@@ -254,3 +254,42 @@ def gather_tokens(pool: torch.Tensor, block_table, num_tokens: int, out: torch.T
 def scatter_tokens(pool: torch.Tensor, block_table, num_tokens: int, src: torch.Tensor, stream=None):
     """pool[:, :, block_table[t // BS], t % BS] = src[:, :, t] for t < num_tokens (kv_handoff.py:112-118)."""
     _token_copy(False, pool, block_table, num_tokens, src, stream)
+
+
+def _token_fp8(gather: bool, pool: torch.Tensor, block_table, num_tokens: int, payload: torch.Tensor,
+               scale: torch.Tensor, stream=None):
+    if pool.ndim != 6 or pool.dtype != torch.bfloat16:
+        raise ValueError("pool must be a bfloat16 [2, layers, blocks, block_size, heads, head_dim] tensor")
+    shape = (2, pool.shape[1], num_tokens, *pool.shape[-2:])
+    if tuple(payload.shape) != shape or payload.dtype != torch.float8_e4m3fn or not payload.is_contiguous():
+        raise ValueError(f"payload must be a contiguous float8_e4m3fn tensor of shape {shape}")
+    if (tuple(scale.shape) != (*shape[:-1], 1) or scale.dtype not in SCALE_DTYPES
+            or not scale.is_contiguous()):
+        raise ValueError(f"scale must be a contiguous bfloat16/float32 tensor of shape {(*shape[:-1], 1)}")
+    for t in (payload, scale):
+        if t.device.type == "cuda":
+            _require_device(pool, t)
+        elif not (gather and t.is_pinned()):
+            raise ValueError("an FP8 gather may write pinned host memory; a scatter reads device memory")
+    device = _require_device(pool)
+    table = list(block_table)
+    fn = lib().kvx_gather_tokens_fp8 if gather else lib().kvx_scatter_tokens_fp8
+    check(fn(pool.data_ptr(), ctypes.byref(pool_layout(pool, scale.dtype)), int32_array(table), len(table),
+             num_tokens * pool.shape[4], payload.data_ptr(), scale.data_ptr(), _stream(device, stream)),
+          "gather_tokens_fp8" if gather else "scatter_tokens_fp8")
+
+
+def gather_tokens_fp8(pool: torch.Tensor, block_table, num_tokens: int, payload: torch.Tensor, scale: torch.Tensor,
+                      stream=None):
+    """fp8_quantize of gather_tokens' [2, L, num_tokens, H, hd] payload, without the BF16 intermediate.
+
+    payload: float8_e4m3fn [2, L, num_tokens, H, hd]; scale: [2, L, num_tokens, H, 1] in bfloat16 or float32,
+    both on the pool's device or in pinned host memory.
+    """
+    _token_fp8(True, pool, block_table, num_tokens, payload, scale, stream)
+
+
+def scatter_tokens_fp8(pool: torch.Tensor, block_table, num_tokens: int, payload: torch.Tensor, scale: torch.Tensor,
+                       stream=None):
+    """pool[:, :, block_table[t // BS], t % BS] = fp8_dequantize(payload, scale)[:, :, t] (device tensors)."""
+    _token_fp8(False, pool, block_table, num_tokens, payload, scale, stream)

@@ -163,3 +163,22 @@ def scatter_block(pool: np.ndarray, block_id: int, payload: np.ndarray):
 def save_block_fp8(pool_bits: np.ndarray, block_id: int, scale_fp32: bool):
     """FP8 entry (codes, scales) of pool block `block_id` (cpu_prefix_cache.py:315-317 via :225-234)."""
     return quantize(gather_block(pool_bits, block_id), scale_fp32)
+
+
+def gather_tokens(pool: np.ndarray, table, count: int) -> np.ndarray:
+    """[2, L, count, H, hd]: the first `count` tokens of the blocks `table` in order (kv_handoff.py:51-55,
+    index_select over the block table, flattened, then sliced)."""
+    table = list(table)
+    picked = pool[:, :, table]
+    return np.ascontiguousarray(picked.reshape(pool.shape[0], pool.shape[1], len(table) * pool.shape[3],
+                                               *pool.shape[4:])[:, :, :count])
+
+
+def scatter_tokens(pool: np.ndarray, table, dense: np.ndarray):
+    """In place: the inverse of gather_tokens for dense's tokens (kv_handoff.py:112-118)."""
+    count, bs = dense.shape[2], pool.shape[3]
+    for i, block in enumerate(table):
+        lo, hi = i * bs, min((i + 1) * bs, count)
+        if lo >= hi:
+            break
+        pool[:, :, block, :hi - lo] = dense[:, :, lo:hi]

@@ -9,14 +9,29 @@ through kvx.ops.store_kvcache and the engine's slot mapping, so the paged
 write runs in the engine loop.
 """
 
+from dataclasses import dataclass
+
 import torch
 
 from kvx import ops
 from kvx.engine.block_manager import BlockManager
-from kvx.engine.llm_engine import LLMEngine, decode_slot_mapping, prefill_slot_mapping
+from kvx.engine.llm_engine import LLMEngine
 from kvx.engine.sequence import SamplingParams
+from kvx.engine.slot_mapping import decode_slot_mapping, prefill_slot_mapping, upload
 
 BS = 256
+
+
+@dataclass
+class Step:
+    """engine.step()'s (outputs, num_tokens) by name."""
+
+    outputs: list
+    num_tokens: int
+
+
+def step(engine) -> Step:
+    return Step(*engine.step())
 
 
 class ScriptedRunner:
@@ -49,12 +64,12 @@ class ScriptedRunner:
         else:
             slots = decode_slot_mapping(seqs, BS)
             values = [seq[0] for seq in seqs]
-        if not slots:
+        if not len(slots):
             return
         heads, hd = pool.shape[4], pool.shape[5]
         rows = torch.tensor(values, dtype=torch.float32, device=pool.device)
         kv = rows[:, None, None].expand(len(values), heads, hd).to(pool.dtype).contiguous()
-        mapping = torch.tensor(slots, dtype=torch.int32, device=pool.device)
+        mapping = upload(slots, pool.device)
         for layer in range(pool.shape[1]):
             ops.store_kvcache(kv, kv, pool[0, layer], pool[1, layer], mapping)
 
@@ -89,8 +104,8 @@ def completed_prefix(device, extra_batches=()):
     raw = torch.arange(pool.numel() * 2, dtype=torch.int64, device=device).remainder(256).to(torch.uint8)
     pool.view(torch.uint8).copy_(raw.view(pool.view(torch.uint8).shape))
     engine.add_request([1] * 257, params(max_tokens=2))
-    engine.step_with_events()
-    engine.step_with_events()
+    step(engine)
+    step(engine)
     manager = engine.scheduler.block_manager
     key = manager.compute_hash([1] * BS)
     assert engine.is_finished() and key in manager.hash_to_block_id
@@ -105,7 +120,7 @@ def finite_prefix(device, batches=(), blocks=1, num_blocks=2):
     engine = cached_engine(device, [[90]] * steps + [*batches], num_blocks=num_blocks)
     engine.add_request([1] * (BS * blocks + 1), params(max_tokens=2))
     while not engine.is_finished():
-        engine.step_with_events()
+        step(engine)
     manager = engine.scheduler.block_manager
     keys, h = [], -1
     for _ in range(blocks):
@@ -124,9 +139,9 @@ def new_cache(engine, blocks=1, **kwargs):
 def overwrite_prefix(engine):
     """bench/test_cpu_prefix_cache.py:35-40."""
     engine.add_request([3] * 257, params(max_tokens=1))
-    engine.step_with_events()
+    step(engine)
     engine.add_request([4], params(max_tokens=1))
-    engine.step_with_events()
+    step(engine)
 
 
 def assert_pool_consistent(manager: BlockManager):

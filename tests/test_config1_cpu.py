@@ -9,7 +9,7 @@ import numpy as np
 import torch
 
 from helpers import bf16_bits
-from kvx.workloads import block_selection
+from workloads import block_selection
 from oracle import kvx_oracle as oracle
 from oracle import torch_path
 

@@ -8,7 +8,7 @@ import torch
 
 from kvx.engine.cpu_prefix_cache import CPUBlockCache
 from kvx.engine.llm_engine import LLMEngine
-from kvx.workloads import QWEN3_8B, SyntheticKVRunner, run_agent_pressure
+from workloads import QWEN3_8B, SyntheticKVRunner, run_agent_pressure
 
 pytestmark = pytest.mark.gpu
 

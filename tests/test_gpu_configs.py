@@ -24,7 +24,7 @@ from kvx import ops
 from kvx.engine.block_manager import BlockManager, plan_split
 from kvx.engine.cpu_prefix_cache import CPUBlockCache
 from kvx.engine.sequence import SamplingParams, Sequence
-from kvx.workloads import QWEN3_0_6B, QWEN3_8B, block_selection, fill_normal, fill_student_t
+from workloads import QWEN3_0_6B, QWEN3_8B, block_selection, fill_normal, fill_student_t
 from oracle import kvx_oracle as oracle
 
 pytestmark = pytest.mark.gpu

@@ -16,7 +16,7 @@ import pytest
 import torch
 
 from engine_fixtures import (BS, assert_pool_consistent, block_bytes, cached_engine, completed_prefix,
-                             finite_prefix, new_cache, overwrite_prefix, params, pool_of, slow_copies,
+                             finite_prefix, new_cache, overwrite_prefix, params, pool_of, slow_copies, step,
                              write_scheduled_kv)
 from kvx.engine.cpu_prefix_cache import CPUBlockCache, CPUCacheFullError
 from kvx.engine.sequence import Sequence
@@ -53,7 +53,7 @@ def test_round_trip_survives_recycling_and_reduces_next_turn_prefill(gpu):
     assert manager.blocks[destination_id].ref_count == 0
     assert_pool_consistent(manager)
     request_id = engine.add_request([1] * 257 + [10, 11] + [2] * 10, params(max_tokens=1))
-    result = engine.step_with_events()
+    result = step(engine)
     assert result.num_tokens == 13  # 269 prompt positions minus the restored 256
     assert result.outputs == [(request_id, [12])]
     assert not manager.used_block_ids
@@ -109,7 +109,7 @@ def test_budget_deduplication_and_explicit_discard(gpu):
     assert not cache.save_block(key)  # the CPU copy survives the GPU miss
     engine.model_runner.batches = iter([[92]])
     engine.add_request([6] * 257, params(max_tokens=1))
-    engine.step_with_events()
+    step(engine)
     other = manager.compute_hash([6] * BS)
     with pytest.raises(MemoryError, match="budget"):
         cache.save_block(other)
@@ -140,14 +140,14 @@ def test_restore_without_space_preserves_active_request_and_cpu_entry(gpu):
     cache = new_cache(engine)
     cache.save_block(key)
     engine.add_request([3] * 257, params(max_tokens=2))
-    engine.step_with_events()
+    step(engine)
     before = manager.used_block_ids.copy()
     assert not manager.free_block_ids and key not in manager.hash_to_block_id
     with pytest.raises(MemoryError, match="free KV blocks"):
         cache.restore_block(key)
     assert manager.used_block_ids == before and key in cache
     assert_pool_consistent(manager)
-    engine.step_with_events()
+    step(engine)
     assert cache.restore_block(key) in manager.hash_to_block_id.values()
     assert_pool_consistent(manager)
 
@@ -155,7 +155,7 @@ def test_restore_without_space_preserves_active_request_and_cpu_entry(gpu):
 def test_existing_live_gpu_hit_is_not_overwritten_or_referenced_again(gpu, monkeypatch):
     engine = cached_engine(gpu, [[10]], num_blocks=2)
     engine.add_request([1] * 257, params(max_tokens=2))
-    engine.step_with_events()
+    step(engine)
     manager = engine.scheduler.block_manager
     key = manager.compute_hash([1] * BS)
     cache = new_cache(engine)
@@ -178,19 +178,19 @@ def test_restore_chained_prefix_blocks_preserves_ancestry(gpu):
     manager = engine.scheduler.block_manager
     original = [1] * 256 + [2] * 256 + [3]
     engine.add_request(original, params(max_tokens=1))
-    engine.step_with_events()
+    step(engine)
     first = manager.compute_hash([1] * BS)
     second = manager.compute_hash([2] * BS, first)
     cache = new_cache(engine, blocks=2)
     cache.save_block(first)
     cache.save_block(second)
     engine.add_request([8] * 513, params(max_tokens=1))
-    engine.step_with_events()
+    step(engine)
     assert first not in manager.hash_to_block_id and second not in manager.hash_to_block_id
     cache.restore_block(first)
     cache.restore_block(second)
     engine.add_request(original + [9] * 10, params(max_tokens=1))
-    assert engine.step_with_events().num_tokens == 11
+    assert step(engine).num_tokens == 11
     assert_pool_consistent(manager)
 
 
@@ -323,10 +323,10 @@ def test_automatic_save_restore_and_next_turn_without_manual_calls(gpu):
     write_scheduled_kv(engine)
     for prompt in ([3] * 257, [4]):
         engine.add_request(prompt, params(max_tokens=1))
-        engine.step_with_events()
+        step(engine)
     assert key not in manager.hash_to_block_id and key in cache
     engine.add_request([1] * 257 + [10, 11] + [2] * 10, params(max_tokens=1))
-    assert engine.step_with_events().num_tokens == 13
+    assert step(engine).num_tokens == 13
     target = manager.hash_to_block_id[key]
     assert target != source
     assert torch.equal(block_bytes(engine, target), expected)
@@ -341,7 +341,7 @@ def test_all_gpu_hits_are_protected_before_any_cpu_restore(gpu, cpu_logical):
     manager = engine.scheduler.block_manager
     original = [1] * 256 + [2] * 256 + [3]
     engine.add_request(original, params(max_tokens=1))
-    engine.step_with_events()
+    step(engine)
     first = manager.compute_hash([1] * BS)
     second = manager.compute_hash([2] * BS, first)
     keys = [first, second]
@@ -352,12 +352,12 @@ def test_all_gpu_hits_are_protected_before_any_cpu_restore(gpu, cpu_logical):
     tail = next(i for i in manager.free_block_ids if i not in (victim, gpu_hit))
     manager.free_block_ids = deque([victim, gpu_hit, tail])
     engine.add_request([9], params(max_tokens=1))
-    engine.step_with_events()
+    step(engine)
     assert keys[cpu_logical] in cache
     assert manager.free_block_ids[0] == gpu_hit
     expected = block_bytes(engine, gpu_hit)
     engine.add_request(original + [8] * 10, params(max_tokens=1))
-    assert engine.step_with_events().num_tokens == 11
+    assert step(engine).num_tokens == 11
     assert manager.hash_to_block_id[keys[1 - cpu_logical]] == gpu_hit
     assert torch.equal(block_bytes(engine, gpu_hit), expected)
     assert cache.stats["restored_blocks"] == 1
@@ -369,7 +369,7 @@ def test_cpu_hit_waits_for_capacity_without_mutating_pool_during_lookup(gpu):
     cache = automatic_cache(engine, blocks=1)
     write_scheduled_kv(engine)
     engine.add_request([3] * 257, params(max_tokens=2))
-    engine.step_with_events()
+    step(engine)
     engine.add_request([1] * 257 + [10, 11] + [2] * 10, params(max_tokens=1))
     waiting = engine.scheduler.waiting[0]
     before = (manager.used_block_ids.copy(), manager.hash_to_block_id.copy(), cache.stats)
@@ -377,8 +377,8 @@ def test_cpu_hit_waits_for_capacity_without_mutating_pool_during_lookup(gpu):
     assert manager.can_allocate(waiting) == -1
     assert (manager.used_block_ids, manager.hash_to_block_id, cache.stats) == before
     assert not waiting.block_table
-    assert engine.step_with_events().num_tokens == -1  # the running decode completes
-    assert engine.step_with_events().num_tokens == 13
+    assert step(engine).num_tokens == -1  # the running decode completes
+    assert step(engine).num_tokens == 13
     assert cache.stats["restored_blocks"] == 1
     assert_pool_consistent(manager)
 
@@ -388,10 +388,10 @@ def test_full_cpu_budget_falls_back_to_recomputation(gpu):
     cache = engine.create_cpu_prefix_cache(max_bytes=1, automatic=True)
     for prompt in ([3] * 257, [4]):
         engine.add_request(prompt, params(max_tokens=1))
-        engine.step_with_events()
+        step(engine)
     assert key not in cache and key not in manager.hash_to_block_id
     engine.add_request([1] * 257 + [10, 11] + [2] * 10, params(max_tokens=1))
-    assert engine.step_with_events().num_tokens == 269
+    assert step(engine).num_tokens == 269
     assert cache.stats["budget_skips"] >= 1
     assert cache.stats["saved_blocks"] == cache.stats["restored_blocks"] == 0
     assert_pool_consistent(manager)
@@ -403,11 +403,11 @@ def test_gpu_hits_are_shared_with_active_requests_without_cpu_copy(gpu):
     manager = engine.scheduler.block_manager
     cache = automatic_cache(engine)
     first_id = engine.add_request([1] * 257, params(max_tokens=3))
-    engine.step_with_events()
+    step(engine)
     first = engine.scheduler.running[0]
     block_id = manager.hash_to_block_id[manager.compute_hash([1] * BS)]
     engine.add_request([1] * 257 + [10] + [2] * 10, params(max_tokens=1))
-    assert engine.step_with_events().num_tokens == 12
+    assert step(engine).num_tokens == 12
     assert first.seq_id == first_id and manager.blocks[block_id].ref_count == 1
     assert cache.stats == {"saved_blocks": 0, "restored_blocks": 0, "budget_skips": 0}
     assert_pool_consistent(manager)
@@ -436,17 +436,17 @@ def test_failed_later_admission_keeps_already_prefilled_chunks(gpu, monkeypatch)
     engine = cached_engine(gpu, [[20], [90], [91], [92], [10], [13, 14]], budget=512, num_blocks=5)
     manager = engine.scheduler.block_manager
     engine.add_request([3] * 257, params(max_tokens=1))
-    engine.step_with_events()
+    step(engine)
     cache = automatic_cache(engine, blocks=2)
     key = manager.compute_hash([3] * BS)
     cache.save_block(key)
     engine.add_request([9] * 1025, params(max_tokens=1))
     for _ in range(3):
-        engine.step_with_events()
+        step(engine)
     assert key not in manager.hash_to_block_id
     first_id = engine.add_request([1] * 513, params(max_tokens=1))
     second_id = engine.add_request([3] * 257, params(max_tokens=1))
-    engine.step_with_events()  # the first request's first 512 tokens are prefilled
+    step(engine)  # the first request's first 512 tokens are prefilled
     first = engine.scheduler.waiting[0]
     blocks = first.block_table.copy()
     assert first.num_cached_tokens == 512
@@ -457,13 +457,13 @@ def test_failed_later_admission_keeps_already_prefilled_chunks(gpu, monkeypatch)
     with monkeypatch.context() as patch:
         patch.setattr(cache, "_copy_entry", fail)
         with pytest.raises(RuntimeError, match="restore failed"):
-            engine.step_with_events()
+            step(engine)
     assert [seq.seq_id for seq in engine.scheduler.waiting] == [first_id, second_id]
     assert not engine.scheduler.running
     assert first.block_table == blocks and first.num_cached_tokens == 512 and first.num_scheduled_tokens == 0
     assert manager.used_block_ids == set(blocks)
     assert_pool_consistent(manager)
-    result = engine.step_with_events()
+    result = step(engine)
     assert result.num_tokens == 2
     assert result.outputs == [(first_id, [13]), (second_id, [14])]
     assert not manager.used_block_ids
@@ -475,7 +475,7 @@ def test_cpu_hits_do_not_make_an_oversized_active_request_fit(gpu):
     cache = automatic_cache(engine, blocks=1)
     for prompt in ([3] * 257, [4]):
         engine.add_request(prompt, params(max_tokens=1))
-        engine.step_with_events()
+        step(engine)
     assert key in cache and key not in manager.hash_to_block_id
     seq = Sequence([1] * 513, params(max_tokens=1))
     before = (list(manager.free_block_ids), cache.stats)
@@ -490,7 +490,7 @@ def test_repeated_admission_checks_do_not_rehash_a_waiting_prompt(gpu, monkeypat
     cache = automatic_cache(engine, blocks=1)
     for prompt in ([3] * 257, [4]):
         engine.add_request(prompt, params(max_tokens=1))
-        engine.step_with_events()
+        step(engine)
     assert key in cache and key not in manager.hash_to_block_id
     seq = Sequence([1] * 257, params(max_tokens=1))
     assert manager.can_allocate(seq) == 1
@@ -509,28 +509,26 @@ def test_close_detaches_automatic_hooks(gpu):
     assert not cache.automatic and manager._cpu_prefix_cache is None
     for prompt in ([3] * 257, [4]):
         engine.add_request(prompt, params(max_tokens=1))
-        engine.step_with_events()
+        step(engine)
     engine.add_request([1] * 257 + [10, 11] + [2] * 10, params(max_tokens=1))
-    assert engine.step_with_events().num_tokens == 269
+    assert step(engine).num_tokens == 269
     assert cache.stats["saved_blocks"] == 0
 
 
-@pytest.mark.parametrize("policy", ["legacy", "fixed", "decode_aware"])
-def test_prefill_batch_restore_failure_rolls_back_all_admissions(gpu, monkeypatch, policy):
-    engine = cached_engine(gpu, [[10], [20], [90], [13, 14]], budget=1024, num_blocks=4,
-                           prefill_policy=policy, prefill_chunk_size=1024)
+def test_prefill_batch_restore_failure_rolls_back_all_admissions(gpu, monkeypatch):
+    engine = cached_engine(gpu, [[10], [20], [90], [13, 14]], budget=1024, num_blocks=4)
     manager = engine.scheduler.block_manager
     engine.add_request([1] * 257, params(max_tokens=1))
-    engine.step_with_events()
+    step(engine)
     cache = automatic_cache(engine, blocks=2)
     first = manager.compute_hash([1] * BS)
     cache.save_block(first)
     engine.add_request([3] * 257, params(max_tokens=1))
-    engine.step_with_events()
+    step(engine)
     second = manager.compute_hash([3] * BS)
     cache.save_block(second)
     engine.add_request([9] * 769, params(max_tokens=1))
-    engine.step_with_events()
+    step(engine)
     assert first not in manager.hash_to_block_id and second not in manager.hash_to_block_id
     ids = [engine.add_request([value] * 257, params(max_tokens=1)) for value in (1, 3)]
     calls = []
@@ -546,30 +544,28 @@ def test_prefill_batch_restore_failure_rolls_back_all_admissions(gpu, monkeypatc
     with monkeypatch.context() as patch:
         patch.setattr(cache, "_copy_entry", fail_second)
         with pytest.raises(RuntimeError, match="restore failed"):
-            engine.step_with_events()
+            step(engine)
     assert [seq.seq_id for seq in engine.scheduler.waiting] == ids
     assert not engine.scheduler.running and not manager.used_block_ids
     assert all(not seq.block_table and seq.num_cached_tokens == seq.num_scheduled_tokens == 0
                for seq in engine.scheduler.waiting)
     assert len([c for c in engine.model_runner.calls if c != "exit"]) == 3
     assert_pool_consistent(manager)
-    result = engine.step_with_events()
+    result = step(engine)
     assert result.num_tokens == 2  # one uncached tail token per 257-token prompt
     assert result.outputs == [(ids[0], [13]), (ids[1], [14])]
     assert_pool_consistent(manager)
 
 
-@pytest.mark.parametrize("policy", ["legacy", "fixed", "decode_aware"])
-def test_decode_growth_failure_restores_queue_and_tail_reservations(gpu, monkeypatch, policy):
-    engine = cached_engine(gpu, [[80], [81], [10, 20], [11, 21]], budget=512, num_blocks=4,
-                           prefill_policy=policy, prefill_chunk_size=512)
+def test_decode_growth_failure_restores_queue_and_tail_reservations(gpu, monkeypatch):
+    engine = cached_engine(gpu, [[80], [81], [10, 20], [11, 21]], budget=512, num_blocks=4)
     manager = engine.scheduler.block_manager
     for value in (7, 8):
         engine.add_request([value] * 256, params(max_tokens=1))
-        engine.step_with_events()
+        step(engine)
     cache = automatic_cache(engine, blocks=2)
     ids = [engine.add_request([value] * 256, params(max_tokens=2)) for value in (1, 2)]
-    engine.step_with_events()
+    step(engine)
     before = manager.used_block_ids.copy()
     original = cache.save_block
     count = 0
@@ -584,12 +580,12 @@ def test_decode_growth_failure_restores_queue_and_tail_reservations(gpu, monkeyp
     with monkeypatch.context() as patch:
         patch.setattr(cache, "save_block", fail_second)
         with pytest.raises(RuntimeError, match="preservation failed"):
-            engine.step_with_events()
+            step(engine)
     assert [seq.seq_id for seq in engine.scheduler.running] == ids
     assert manager.used_block_ids == before
     assert all(len(seq.block_table) == 1 and seq.num_scheduled_tokens == 0 for seq in engine.scheduler.running)
     assert_pool_consistent(manager)
-    assert engine.step_with_events().outputs == [(ids[0], [10, 11]), (ids[1], [20, 21])]
+    assert step(engine).outputs == [(ids[0], [10, 11]), (ids[1], [20, 21])]
     assert not manager.used_block_ids
     assert_pool_consistent(manager)
 
@@ -605,17 +601,17 @@ def test_save_on_release_saves_idle_blocks_before_recycling_overwrites_them(gpu,
         slow_copies(cache)
     write_scheduled_kv(engine)
     engine.add_request([1] * 257, params(max_tokens=2))
-    engine.step_with_events()
+    step(engine)
     engine.add_request([3] * 257, params(max_tokens=1))
-    engine.step_with_events()  # [3] waits for blocks while [1] decodes, then [1] releases
+    step(engine)  # [3] waits for blocks while [1] decodes, then [1] releases
     key = manager.compute_hash([1] * BS)
     assert key in cache and key in manager.hash_to_block_id
     assert cache.stats["saved_blocks"] == 1
     expected = block_bytes(engine, manager.hash_to_block_id[key])
-    engine.step_with_events()  # admitting [3] recycles the source block: the pending save must win
+    step(engine)  # admitting [3] recycles the source block: the pending save must win
     assert engine.is_finished() and key not in manager.hash_to_block_id
     engine.add_request([1] * 257 + [10, 11] + [2] * 10, params(max_tokens=1))
-    assert engine.step_with_events().num_tokens == 13
+    assert step(engine).num_tokens == 13
     target = manager.hash_to_block_id[key]
     assert torch.equal(block_bytes(engine, target), expected)
     assert cache.stats["saved_blocks"] == cache.stats["restored_blocks"] == 1
@@ -629,8 +625,8 @@ def test_save_on_release_waits_for_blocked_admission(gpu):
     size = pool[:, :, 0].numel() * pool.element_size()
     cache = engine.create_cpu_prefix_cache(max_bytes=size, automatic=True, save_on_release=True)
     engine.add_request([1] * 257, params(max_tokens=2))
-    engine.step_with_events()
-    engine.step_with_events()
+    step(engine)
+    step(engine)
     assert engine.is_finished() and cache.stats["saved_blocks"] == 0
 
 
@@ -645,7 +641,7 @@ def test_prefetch_restores_blocked_waiting_hits_while_others_decode(gpu, slow):
         slow_copies(cache)
     write_scheduled_kv(engine)
     engine.add_request([1] * 257, params(max_tokens=1))
-    engine.step_with_events()
+    step(engine)
     key = manager.compute_hash([1] * BS)
     source = manager.hash_to_block_id[key]
     expected = block_bytes(engine, source)
@@ -655,13 +651,13 @@ def test_prefetch_restores_blocked_waiting_hits_while_others_decode(gpu, slow):
     manager.blocks[source].hash, manager.blocks[source].token_ids = -1, []
     pool[:, :, source].zero_()
     engine.add_request([3] * 257, params(max_tokens=3))
-    engine.step_with_events()  # the running request holds 2 of 4 blocks
+    step(engine)  # the running request holds 2 of 4 blocks
     waiting = engine.add_request([1] * 256 + [5] * 300, params(max_tokens=1))
-    engine.step_with_events()  # needs 3 blocks; one spare block prefetches its hit
+    step(engine)  # needs 3 blocks; one spare block prefetches its hit
     assert key in manager.hash_to_block_id and cache.prefetched_blocks == 1
     assert [seq.seq_id for seq in engine.scheduler.waiting] == [waiting]
-    engine.step_with_events()
-    result = engine.step_with_events()
+    step(engine)
+    result = step(engine)
     assert result.num_tokens == 300  # admitted with the prefetched block as a GPU hit
     target = manager.hash_to_block_id[key]
     assert torch.equal(block_bytes(engine, target), expected)
@@ -767,14 +763,14 @@ def test_split_admission_recomputes_head_while_restoring_tail(gpu, slow):
         slow_copies(cache)
     write_scheduled_kv(engine)
     request = engine.add_request([1] * 768 + [5] * 10, params(max_tokens=1))
-    head = engine.step_with_events()
+    head = step(engine)
     seq = next(seq for seq in engine.scheduler.waiting if seq.seq_id == request)
     assert head.num_tokens == 256 and seq.restore_span is None and seq.num_cached_tokens == 768
     assert cache.stats["restored_blocks"] == 2
     assert torch.equal(block_bytes(engine, seq.block_table[1]), expected[1])
     assert torch.equal(block_bytes(engine, seq.block_table[2]), expected[2])
     assert manager.hash_to_block_id[keys[0]] == seq.block_table[0]
-    tail = engine.step_with_events()
+    tail = step(engine)
     assert tail.num_tokens == 10 and tail.outputs
     assert engine.is_finished() and not manager.used_block_ids
     assert_pool_consistent(manager)
@@ -807,11 +803,11 @@ def test_later_requests_join_the_step_of_a_split_admission_head(gpu):
     drop_gpu_copies(cache, manager, pool, keys)
     split = engine.add_request([1] * 768 + [5] * 10, params(max_tokens=1))
     short = engine.add_request([8] * 10, params(max_tokens=1))
-    step = engine.step_with_events()
-    assert step.num_tokens == 256 + 10
+    first = step(engine)
+    assert first.num_tokens == 256 + 10
     assert [seq.seq_id for seq in engine.scheduler.waiting] == [split]
-    assert [event.seq_id for event in step.token_events] == [short]
-    assert engine.step_with_events().num_tokens == 10
+    assert first.outputs == [(short, [91])]  # the split head samples nothing yet; the short request finishes
+    assert step(engine).num_tokens == 10
     assert engine.is_finished()
     assert_pool_consistent(manager)
 
@@ -825,7 +821,7 @@ def test_split_admission_that_recomputes_everything_uses_no_restore(gpu):
     cache.hybrid = (1.0, 0, 0)  # recompute is free
     drop_gpu_copies(cache, manager, pool, keys)
     request = engine.add_request([1] * 512 + [5], params(max_tokens=1))
-    engine.step_with_events()
+    step(engine)
     seq = next(seq for seq in engine.scheduler.waiting if seq.seq_id == request)
     assert seq.num_cached_tokens == 512 and seq.restore_span is None  # computed, not skipped
     assert cache.stats["restored_blocks"] == 0
@@ -843,15 +839,15 @@ def test_hybrid_requires_automatic_cache(gpu):
 
 @pytest.mark.parametrize("fp8", [False, True])
 def test_cpu_restoration_and_prefill_budget_compose(gpu, fp8):
-    """bench/test_prefill_scheduling.py:178-193: a CPU hit admitted under a fixed
-    prefill budget is restored once, then its uncached tail is prefilled in
+    """bench/test_prefill_scheduling.py:178-193: a CPU hit admitted under a small
+    prefill token budget is restored once, then its uncached tail is prefilled in
     budget-sized chunks. The restored block also holds the saved bytes (BF16
-    byte-exact, FP8 within the reference's per-row bound)."""
-    engine = cached_engine(gpu, [[10], [90], [91], [92], [12]], budget=512, num_blocks=2,
-                           prefill_policy="fixed", prefill_chunk_size=512)
+    byte-exact, FP8 within the reference's per-row bound). The reference sets the
+    budget through its chunked prefill policy; here it is the batch token budget."""
+    engine = cached_engine(gpu, [[10], [90], [91], [92], [12]], budget=512, num_blocks=2)
     manager = engine.scheduler.block_manager
     engine.add_request([1] * 257, params(max_tokens=1))
-    engine.step_with_events()
+    step(engine)
     key = manager.compute_hash([1] * BS)
     pool = pool_of(engine)
     before = pool[:, :, manager.hash_to_block_id[key]].clone()
@@ -859,11 +855,11 @@ def test_cpu_restoration_and_prefill_budget_compose(gpu, fp8):
     cache = engine.create_cpu_prefix_cache(size, automatic=True, fp8=fp8)
     for value, length in ((3, 257), (4, 1)):
         engine.add_request([value] * length, params(max_tokens=1))
-        engine.step_with_events()
+        step(engine)
     assert key not in manager.hash_to_block_id and key in cache
-    engine.scheduler.prefill_chunk_size = 8
+    engine.scheduler.max_num_batched_tokens = 8
     engine.add_request([1] * 269, params(max_tokens=1))
-    assert engine.step_with_events().num_tokens == 8
+    assert step(engine).num_tokens == 8
     assert cache.stats["restored_blocks"] == 1
     torch.cuda.synchronize(pool.device)
     after = pool[:, :, manager.hash_to_block_id[key]]
@@ -872,6 +868,6 @@ def test_cpu_restoration_and_prefill_budget_compose(gpu, fp8):
         assert bool(((after.float() - before.float()).abs() <= row_amax / 16).all())
     else:
         assert torch.equal(after.view(torch.int16), before.view(torch.int16))
-    assert engine.step_with_events().num_tokens == 5
+    assert step(engine).num_tokens == 5
     assert engine.is_finished()
     assert_pool_consistent(manager)

@@ -1,60 +1,91 @@
-"""KV handoff (detach/export, resume/import) over libkvx's token copies.
+"""KV handoff on a ROCm pool: the token-copy kernels (BF16 and FP8) and the engine's detach/resume.
 
-Restates bench/test_engine_handoff.py on a ROCm pool, and checks the token
-gather/scatter kernels against the reference's own formulation of the same
+The kernels are checked against the oracle's closed form of the reference's
 copy (index_select over the block table, then a slice; kv_handoff.py:51-55)
-evaluated in numpy.
+and, for FP8, the oracle's codec (cpu_prefix_cache.py:20-28) applied to it.
+The engine tests cover bench/test_engine_handoff.py's scenarios for both
+payload formats.
 """
 
 from dataclasses import replace
-from types import SimpleNamespace
 
 import numpy as np
 import pytest
 import torch
 
 import kvx.engine.kv_handoff as kv_handoff
-from engine_fixtures import cached_engine, params
+from engine_fixtures import cached_engine, params, step
+from helpers import bf16_bits, finite_bf16_rows
 from kvx import ops
-from kvx.engine.llm_engine import TokenEvent
-from kvx.engine.sequence import Sequence
+from oracle import kvx_oracle as oracle
 
 pytestmark = pytest.mark.gpu
 
+SHAPES = [((2, 3, 300, 256, 2, 128), 300 * 256 - 77),  # > 128 blocks per call, ragged last block
+          ((2, 2, 6, 256, 1, 4), 1),                   # the reference tests' geometry (generic kernels)
+          ((2, 2, 6, 256, 1, 4), 513),
+          ((2, 4, 9, 256, 8, 128), 2 * 256),           # exact blocks
+          ((2, 2, 5, 256, 8, 128), 256 + 3)]
 
-def bytes_of(t):
-    return t.contiguous().cpu().view(torch.uint8).numpy()
 
-
-@pytest.mark.parametrize("shape,tokens", [((2, 3, 300, 256, 2, 128), 300 * 256 - 77),  # > 128 blocks, ragged
-                                          ((2, 2, 6, 256, 1, 4), 1),
-                                          ((2, 2, 6, 256, 1, 4), 513),
-                                          ((2, 4, 9, 256, 8, 128), 2 * 256)])
-def test_token_gather_and_scatter_match_the_index_select_formulation(gpu, shape, tokens):
-    g = torch.Generator(device=gpu).manual_seed(tokens)
+def random_pool(gpu, shape, seed, finite=False):
     pool = torch.empty(shape, dtype=torch.bfloat16, device=gpu)
-    pool.view(torch.int16).random_(-32768, 32768, generator=g)
-    nb, bs = shape[2], shape[3]
-    need = -(-tokens // bs)
-    table = torch.randperm(nb, generator=torch.Generator().manual_seed(1))[:need].tolist()
+    if finite:
+        rows = finite_bf16_rows(pool.numel() // shape[-1], shape[-1], seed)
+        pool.view(torch.int16).copy_(torch.from_numpy(rows.view(np.int16)).view(shape))
+    else:
+        pool.view(torch.int16).random_(-32768, 32768, generator=torch.Generator(device=gpu).manual_seed(seed))
+    return pool
+
+
+def table_for(shape, tokens, seed=1):
+    need = -(-tokens // shape[3])
+    return torch.randperm(shape[2], generator=torch.Generator().manual_seed(seed))[:need].tolist()
+
+
+@pytest.mark.parametrize("shape,tokens", SHAPES)
+def test_token_gather_and_scatter_match_the_index_select_formulation(gpu, shape, tokens):
+    pool = random_pool(gpu, shape, tokens)
+    table = table_for(shape, tokens)
+    host = bf16_bits(pool)
+    expect = oracle.gather_tokens(host, table, tokens)
     out = torch.empty((2, shape[1], tokens, *shape[-2:]), dtype=pool.dtype, device=gpu)
     ops.gather_tokens(pool, table, tokens, out)
-    host = pool.cpu().view(torch.int16).numpy()
-    expect = host[:, :, table].reshape(2, shape[1], need * bs, *shape[-2:])[:, :, :tokens]
-    assert np.array_equal(out.cpu().view(torch.int16).numpy(), expect)
+    assert np.array_equal(bf16_bits(out), expect)
     pinned = torch.empty(out.shape, dtype=out.dtype, pin_memory=True)
-    ops.gather_tokens(pool, table, tokens, pinned)  # straight into mapped host memory
+    ops.gather_tokens(pool, table, tokens, pinned)  # straight into pinned host memory
     torch.cuda.synchronize()
-    assert np.array_equal(pinned.view(torch.int16).numpy(), expect)
-    # Scatter into a fresh pool: exactly the tokens' rows change.
+    assert np.array_equal(pinned.view(torch.int16).numpy().view(np.uint16), expect)
     dest = torch.zeros_like(pool)
     ops.scatter_tokens(dest, table, tokens, out)
-    got = dest.cpu().view(torch.int16).numpy()
     want = np.zeros_like(host)
-    flat = want[:, :, table].reshape(2, shape[1], need * bs, *shape[-2:])
-    flat[:, :, :tokens] = expect
-    want[:, :, table] = flat.reshape(2, shape[1], need, bs, *shape[-2:])
-    assert np.array_equal(got, want)
+    oracle.scatter_tokens(want, table, expect)
+    assert np.array_equal(bf16_bits(dest), want)  # exactly the tokens' rows change
+
+
+@pytest.mark.parametrize("scale_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape,tokens", SHAPES)
+def test_fp8_token_gather_is_the_codec_of_the_gathered_tokens(gpu, shape, tokens, scale_dtype):
+    pool = random_pool(gpu, shape, tokens + 7, finite=True)
+    table = table_for(shape, tokens, seed=3)
+    fp32 = scale_dtype == torch.float32
+    codes, scales = oracle.quantize(oracle.gather_tokens(bf16_bits(pool), table, tokens), fp32)
+    dense = (2, shape[1], tokens, *shape[-2:])
+    for where in ("device", "pinned"):
+        kw = {"device": gpu} if where == "device" else {"pin_memory": True}
+        payload = torch.empty(dense, dtype=torch.float8_e4m3fn, **kw)
+        scale = torch.empty((*dense[:-1], 1), dtype=scale_dtype, **kw)
+        ops.gather_tokens_fp8(pool, table, tokens, payload, scale)
+        torch.cuda.synchronize()
+        assert np.array_equal(payload.cpu().view(torch.uint8).numpy(), codes), f"{where} payload"
+        got_scales = scale.cpu().view(torch.int32 if fp32 else torch.int16).numpy()
+        assert np.array_equal(got_scales, scales.view(np.int32 if fp32 else np.int16)), f"{where} scales"
+    # Scatter (dequantise) into a fresh pool: exactly the tokens' rows change, to the oracle's dequantisation.
+    dest = torch.zeros_like(pool)
+    ops.scatter_tokens_fp8(dest, table, tokens, payload.to(gpu), scale.to(gpu))
+    want = np.zeros(shape, dtype=np.uint16)
+    oracle.scatter_tokens(want, table, oracle.dequantize(codes, scales, fp32))
+    assert np.array_equal(bf16_bits(dest), want)
 
 
 def test_token_copies_reject_short_tables_and_bad_buffers(gpu):
@@ -68,144 +99,172 @@ def test_token_copies_reject_short_tables_and_bad_buffers(gpu):
         ops.gather_tokens(pool, [0, 1], 299, out)
     with pytest.raises(ValueError, match="pinned"):
         ops.gather_tokens(pool, [0, 1], 300, torch.empty(out.shape, dtype=out.dtype))
+    payload = torch.empty(out.shape, dtype=torch.float8_e4m3fn, device=gpu)
+    scale = torch.empty((*out.shape[:-1], 1), dtype=torch.float32, device=gpu)
+    with pytest.raises(IndexError, match="need 2 blocks"):
+        ops.gather_tokens_fp8(pool, [3], 300, payload, scale)
+    with pytest.raises(ValueError, match="twice"):
+        ops.scatter_tokens_fp8(pool, [1, 1], 300, payload, scale)
+    with pytest.raises(ValueError, match="scatter reads device memory"):
+        ops.scatter_tokens_fp8(pool, [0, 1], 300, payload.cpu().pin_memory(), scale)
 
 
-def prefilled_engine(gpu, length=5, max_tokens=3, batches=None):
-    engine = cached_engine(gpu, batches or [[10]])
-    request_id = engine.add_request([1] * length, params(max_tokens=max_tokens))
-    engine.step_with_events()
-    return engine, request_id
+def running_request(gpu, length=5, max_tokens=3, batches=None, **engine):
+    """An engine whose only request has been prefilled (one completion token, one pending)."""
+    engine_ = cached_engine(gpu, batches or [[10]], **engine)
+    request_id = engine_.add_request([1] * length, params(max_tokens=max_tokens))
+    step(engine_)
+    return engine_, request_id
 
 
-def test_detach_preserves_source_blocks_and_other_requests_can_progress(gpu):
-    source, request_id = prefilled_engine(gpu, batches=[[10], [20]])
-    original = source.scheduler.running[0]
-    blocks = original.block_table.copy()
-    snapshot = source.detach_request(request_id)
-    assert snapshot.token_ids == [1] * 5 + [10] and snapshot.num_cached_tokens == 5
-    assert source._detached_requests[request_id] is original and original.block_table == blocks
-    assert source.scheduler.block_manager.used_block_ids == set(blocks)
+FORMATS = [pytest.param({}, id="bf16"), pytest.param({"fp8": True}, id="fp8-fp32"),
+           pytest.param({"fp8": True, "scale_dtype": torch.bfloat16}, id="fp8-bf16")]
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("length", [255, 256, 257])
+def test_detach_then_resume_carries_the_kv_and_decode_continues(gpu, length, fmt):
+    source, source_id = running_request(gpu, length=length)
+    pool = source.model_runner.kv_cache
+    table = source.scheduler.running[0].block_table.copy()
+    snapshot = source.detach_request(source_id, **fmt)
+    tokens = oracle.gather_tokens(bf16_bits(pool), table, length)
+    if fmt:
+        fp32 = fmt.get("scale_dtype", torch.float32) == torch.float32
+        codes, scales = oracle.quantize(tokens, fp32)
+        assert np.array_equal(snapshot.kv.view(torch.uint8).numpy(), codes)
+        assert np.array_equal(snapshot.scale.view(torch.uint8).numpy(), scales.view(np.uint8))
+        assert snapshot.payload_bytes == codes.nbytes + scales.nbytes  # about half of the BF16 payload
+        tokens = oracle.dequantize(codes, scales, fp32)
+    else:
+        assert np.array_equal(snapshot.kv.view(torch.int16).numpy().view(np.uint16), tokens)
+    assert snapshot.token_ids == [1] * length + [10] and snapshot.num_cached_tokens == length
+    assert source.scheduler.block_manager.used_block_ids == set(table)  # the source keeps its blocks
+    destination = cached_engine(gpu, [[11], [12]])
+    destination.model_runner.kv_cache.fill_(-1)
+    destination_id = destination.resume_request(snapshot)
+    seq = destination.scheduler.running[0]
+    assert destination_id == seq.seq_id != source_id
+    assert not seq.is_prefill and seq.num_cached_tokens == length and seq.completion_token_ids == [10]
+    assert len(seq.block_table) == -(-length // 256)
+    assert np.array_equal(oracle.gather_tokens(bf16_bits(destination.model_runner.kv_cache), seq.block_table,
+                                               length), tokens)
+    assert kv_handoff.verify_imported_kv(destination.model_runner, seq, snapshot)
+    manager = destination.scheduler.block_manager
+    assert (manager.blocks[seq.block_table[0]].hash != -1) == (length >= 256)  # full blocks are published
+    source.release_detached_request(source_id)
+    assert step(destination).num_tokens == -1
+    final = step(destination)
+    assert final.outputs == [(destination_id, [10, 11, 12])]
+    assert all(not prefill for prefill, _ in destination.model_runner.calls)
+    assert not manager.used_block_ids
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_import_leaves_the_payload_free_for_reuse(gpu, fmt):
+    """Once resume_request returns, the snapshot's pinned memory may be dropped and reused at once."""
+    source, source_id = running_request(gpu, length=700, budget=1024)
+    snapshot = source.detach_request(source_id, **fmt)
+    expected = kv_handoff.KVSnapshot(**{**snapshot.__dict__, "kv": snapshot.kv.clone(),
+                                        "scale": None if snapshot.scale is None else snapshot.scale.clone()})
+    destination = cached_engine(gpu, [[11]])
+    destination.resume_request(snapshot)
+    nbytes = snapshot.payload_bytes
+    del snapshot
+    for _ in range(4):  # the host allocator hands the freed pinned blocks out again
+        junk = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+        junk.fill_(0x5A)
+    seq = destination.scheduler.running[0]
+    assert kv_handoff.verify_imported_kv(destination.model_runner, seq, expected)
+
+
+def test_reattach_continues_the_original_request(gpu):
+    source, request_id = running_request(gpu, batches=[[10], [11], [12]])
+    source.detach_request(request_id)
     assert source.is_finished()
+    assert source.reattach_request(request_id) == request_id
+    assert step(source).outputs == []
+    assert step(source).outputs == [(request_id, [10, 11, 12])]
+    assert not source.scheduler.block_manager.used_block_ids
+
+
+def test_other_requests_progress_while_one_is_detached(gpu):
+    source, request_id = running_request(gpu, batches=[[10], [20]])
+    blocks = set(source.scheduler.running[0].block_table)
+    source.detach_request(request_id)
     other = source.add_request([2], params(max_tokens=1))
-    result = source.step_with_events()
-    assert result.token_events == [TokenEvent(other, 0, 20, True)]
+    assert step(source).outputs == [(other, [20])]
     with pytest.raises(ValueError, match="already detached"):
         source.detach_request(request_id)
+    assert source.scheduler.block_manager.used_block_ids == blocks
     source.release_detached_request(request_id)
-    assert not source._detached_requests and not source.scheduler.block_manager.used_block_ids
+    assert not source.scheduler.block_manager.used_block_ids
     with pytest.raises(KeyError):
         source.release_detached_request(request_id)
     with pytest.raises(KeyError):
         source.reattach_request(request_id)
 
 
-def test_reattach_continues_original_id_and_output_position(gpu):
-    source, request_id = prefilled_engine(gpu, batches=[[10], [11], [12]])
-    source.detach_request(request_id)
-    assert source.reattach_request(request_id) == request_id
-    assert source.step_with_events().token_events == [TokenEvent(request_id, 1, 11, False)]
-    final = source.step_with_events()
-    assert final.token_events == [TokenEvent(request_id, 2, 12, True)]
-    assert final.outputs == [(request_id, [10, 11, 12])]
-    assert not source.scheduler.block_manager.used_block_ids
+def test_a_failed_export_keeps_the_request_running(gpu, monkeypatch):
+    source, request_id = running_request(gpu)
+    seq = source.scheduler.running[0]
+    blocks = set(seq.block_table)
 
-
-def test_failed_export_keeps_request_running_and_blocks_owned(gpu, monkeypatch):
-    source, request_id = prefilled_engine(gpu)
-    original = source.scheduler.running[0]
-    blocks = set(original.block_table)
-
-    def fail(*args):
+    def fail(*args, **kwargs):
         raise RuntimeError("export failed")
 
     monkeypatch.setattr(kv_handoff, "export_kv", fail)
     with pytest.raises(RuntimeError, match="export failed"):
         source.detach_request(request_id)
-    assert list(source.scheduler.running) == [original] and not source._detached_requests
+    assert list(source.scheduler.running) == [seq]
     assert source.scheduler.block_manager.used_block_ids == blocks
 
 
-def test_detach_rejects_queued_partial_prefill_finished_and_unknown_requests(gpu):
+def test_only_running_requests_between_steps_can_be_detached(gpu):
     source = cached_engine(gpu, [[90], [91], [10]], budget=2)
     request_id = source.add_request([1] * 5, params(max_tokens=1))
     with pytest.raises(ValueError, match="handoff boundary"):
-        source.detach_request(request_id)
-    source.step_with_events()
+        source.detach_request(request_id)  # still waiting
+    step(source)
     with pytest.raises(ValueError, match="handoff boundary"):
-        source.detach_request(request_id)
-    source.step_with_events()
-    source.step_with_events()
-    for rid in (request_id, -1):
+        source.detach_request(request_id)  # partially prefilled
+    step(source)
+    step(source)
+    for rid in (request_id, -1):  # finished, unknown
         with pytest.raises(ValueError, match="handoff boundary"):
             source.detach_request(rid)
-    assert not source._detached_requests and not source.scheduler.block_manager.used_block_ids
+    assert not source.scheduler.block_manager.used_block_ids
 
 
-@pytest.mark.parametrize("length", [255, 256, 257])
-def test_resume_imports_exact_kv_and_continues_decode_without_replaying_first_token(gpu, length):
-    source, source_id = prefilled_engine(gpu, length=length)
-    snapshot = source.detach_request(source_id)
-    pool = source.model_runner.kv_cache
-    table = source._detached_requests[source_id].block_table
-    expect = pool.cpu()[:, :, table].flatten(2, 3)[:, :, :length]
-    assert np.array_equal(bytes_of(snapshot.kv), bytes_of(expect))
-    destination = cached_engine(gpu, [[11], [12]])
-    destination.model_runner.kv_cache.fill_(-1)
-    destination_id = destination.resume_request(snapshot)
-    seq = destination.scheduler.running[0]
-    manager = destination.scheduler.block_manager
-    assert destination_id == seq.seq_id != source_id
-    assert not seq.is_prefill and seq.num_cached_tokens == length and seq.completion_token_ids == [10]
-    assert len(seq.block_table) == (length + 255) // 256
-    assert kv_handoff.verify_imported_kv(destination.model_runner, seq, snapshot)
-    if length >= 256:
-        assert manager.blocks[seq.block_table[0]].hash != -1
-    source.release_detached_request(source_id)
-    first = destination.step_with_events()
-    assert first.num_tokens == -1 and first.token_events == [TokenEvent(destination_id, 1, 11, False)]
-    final = destination.step_with_events()
-    assert final.outputs == [(destination_id, [10, 11, 12])]
-    assert all(not prefill for prefill, _ in destination.model_runner.calls)
-    assert not manager.used_block_ids
-
-
-@pytest.mark.parametrize("mismatch", ["dtype", "block_size", "shape", "finished"])
-def test_resume_rejects_invalid_snapshot_without_admitting_or_allocating(gpu, mismatch):
-    source, request_id = prefilled_engine(gpu)
-    snapshot = source.detach_request(request_id)
-    if mismatch == "dtype":
-        snapshot = replace(snapshot, kv=snapshot.kv.to(torch.float16))
-    elif mismatch == "block_size":
-        snapshot = replace(snapshot, block_size=512)
-    elif mismatch == "shape":
-        snapshot = replace(snapshot, kv=snapshot.kv[:, :, :-1])
-    else:
-        snapshot = replace(snapshot, max_tokens=1)
+@pytest.mark.parametrize("mismatch", ["dtype", "block_size", "shape", "finished", "fp8_without_scale"])
+def test_resume_rejects_a_snapshot_that_does_not_fit_without_allocating(gpu, mismatch):
+    source, request_id = running_request(gpu)
+    snapshot = source.detach_request(request_id, fp8=mismatch == "fp8_without_scale")
+    changed = {"dtype": {"kv": snapshot.kv.to(torch.float16)}, "block_size": {"block_size": 512},
+               "shape": {"kv": snapshot.kv[:, :, :-1]}, "finished": {"max_tokens": 1},
+               "fp8_without_scale": {"scale": None}}[mismatch]
     destination = cached_engine(gpu, [])
     with pytest.raises(ValueError):
-        destination.resume_request(snapshot)
+        destination.resume_request(replace(snapshot, **changed))
     assert destination.is_finished() and not destination.scheduler.block_manager.used_block_ids
-    assert request_id in source._detached_requests
 
 
-def test_resume_out_of_blocks_preserves_existing_destination_and_source_can_reattach(gpu):
-    source, source_id = prefilled_engine(gpu, length=257, batches=[[10], [11], [12]])
+def test_resume_without_free_blocks_leaves_the_destination_as_it_was(gpu):
+    source, source_id = running_request(gpu, length=257, batches=[[10], [11], [12]])
     snapshot = source.detach_request(source_id)
     destination = cached_engine(gpu, [[20]], num_blocks=1)
     existing_id = destination.add_request([2], params(max_tokens=2))
-    destination.step_with_events()
+    step(destination)
     existing = destination.scheduler.running[0]
-    blocks = set(existing.block_table)
     with pytest.raises(MemoryError):
         destination.resume_request(snapshot)
     assert list(destination.scheduler.running) == [existing] and existing.seq_id == existing_id
-    assert destination.scheduler.block_manager.used_block_ids == blocks
+    assert destination.scheduler.block_manager.used_block_ids == set(existing.block_table)
     assert source.reattach_request(source_id) == source_id
-    assert source.step_with_events().token_events == [TokenEvent(source_id, 1, 11, False)]
 
 
-def test_failed_import_releases_allocated_destination_blocks(gpu, monkeypatch):
-    source, request_id = prefilled_engine(gpu, length=256)
+def test_a_failed_import_releases_the_blocks_it_took(gpu, monkeypatch):
+    source, request_id = running_request(gpu, length=256)
     snapshot = source.detach_request(request_id)
     destination = cached_engine(gpu, [])
     manager = destination.scheduler.block_manager
@@ -217,86 +276,12 @@ def test_failed_import_releases_allocated_destination_blocks(gpu, monkeypatch):
     with pytest.raises(RuntimeError, match="import failed"):
         destination.resume_request(snapshot)
     assert destination.is_finished() and not manager.used_block_ids and len(manager.free_block_ids) == 16
-    assert request_id in source._detached_requests
 
 
-@pytest.mark.parametrize("sync_fails", [False, True])
-def test_cuda_import_waits_for_readiness_before_admission_and_rolls_back_on_failure(gpu, monkeypatch, sync_fails):
-    """bench/test_engine_handoff.py:198-233: the device sync precedes admission; its failure releases blocks."""
-    source, request_id = prefilled_engine(gpu)
-    snapshot = source.detach_request(request_id)
-    destination = cached_engine(gpu, [])
-    manager = destination.scheduler.block_manager
-    destination.model_runner.kv_cache = SimpleNamespace(device=gpu)
-    imported, synchronized = [], []
-
-    def fake_import(runner, block_manager, snap):
-        seq = Sequence(snap.token_ids[:snap.num_prompt_tokens], params(max_tokens=3))
-        seq.append_token(10)
-        block_manager.allocate_for_resume(seq, snap.num_cached_tokens)
-        imported.append(seq)
-        return seq
-
-    def synchronize(device):
-        assert device == gpu
-        assert not destination.scheduler.running
-        synchronized.append(device)
-        if sync_fails:
-            raise RuntimeError("copy failed")
-
-    monkeypatch.setattr(kv_handoff, "import_kv", fake_import)
-    monkeypatch.setattr(torch.cuda, "synchronize", synchronize)
-    if sync_fails:
-        with pytest.raises(RuntimeError, match="copy failed"):
-            destination.resume_request(snapshot)
-        assert not destination.scheduler.running and not manager.used_block_ids
-    else:
-        assert destination.resume_request(snapshot) == imported[0].seq_id
-        assert list(destination.scheduler.running) == imported
-    assert synchronized == [gpu]
-
-
-def test_exit_releases_detached_source_blocks(gpu):
-    source, request_id = prefilled_engine(gpu)
+def test_exit_releases_detached_requests(gpu):
+    source, request_id = running_request(gpu)
     source.detach_request(request_id)
     manager = source.scheduler.block_manager
     source.exit()
-    assert not source._detached_requests and not manager.used_block_ids
+    assert not manager.used_block_ids
     assert source.model_runner.calls[-1] == "exit"
-
-
-def test_detach_and_resume_emit_phase_records(gpu, caplog):
-    """bench/test_handoff_timing.py:118-151."""
-    import json
-    import logging
-
-    import kvx.engine.handoff_timing as timing
-
-    caplog.set_level(logging.DEBUG, logger="nanovllm.kv_handoff")
-    timing.enable(True)
-    try:
-        source, source_id = prefilled_engine(gpu, length=5)
-        snapshot = source.detach_request(source_id)
-        records = [json.loads(r.message) for r in caplog.records]
-        assert [r["op"] for r in records] == ["export_kv", "detach_request"]
-        export, detach = records
-        assert set(export["phases_ms"]) == {"gather_blocks", "pack", "copy_to_host"}
-        assert set(detach["phases_ms"]) == {"export", "unschedule"}
-        assert export["num_tokens"] == 5
-        assert snapshot.payload_bytes == export["payload_bytes"] > 0
-
-        caplog.records.clear()
-        destination = cached_engine(gpu, [[11], [12]])
-        destination.model_runner.kv_cache.fill_(-1)
-        destination.resume_request(snapshot)
-        records = [json.loads(r.message) for r in caplog.records]
-        assert [r["op"] for r in records] == ["import_kv", "resume_request"]
-        imported, resume = records
-        assert set(imported["phases_ms"]) == {"validate", "rebuild_sequence", "allocate_blocks", "copy_to_device",
-                                              "scatter_blocks", "publish_cache"}
-        assert set(resume["phases_ms"]) == {"import", "cuda_sync", "admit"}
-        assert resume["seq_id"] == destination.scheduler.running[0].seq_id
-        assert imported["total_ms"] <= resume["phases_ms"]["import"] + 1e-3  # nested: import inside resume's phase
-        assert kv_handoff.verify_imported_kv(destination.model_runner, destination.scheduler.running[0], snapshot)
-    finally:
-        timing.enable(False)

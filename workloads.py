@@ -1,4 +1,5 @@
-"""Seeded synthetic KV pools and block selections for benchmarks and tests.
+"""Synthetic workloads for bench.py and the tests: seeded KV pools, block selections, a model-free runner
+and the multi-agent pressure driver.
 
 Shapes follow the pool layout [2, L, NB, BS, H, hd] (nanovllm/engine/model_runner.py:120).
 Values are generated on the pool's device, one (K/V, layer) plane at a time,
@@ -7,6 +8,7 @@ with a torch.Generator seeded per plane so any plane can be regenerated.
 
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 
@@ -123,9 +125,11 @@ class SyntheticKVRunner:
     """Runner for kvx.engine.llm_engine.LLMEngine that writes every scheduled token's K/V.
 
     call("run", seqs, is_prefill) computes the slot mapping the way
-    nanovllm's ModelRunner does (model_runner.py:156-166, 186), writes
-    synthetic_kv rows for all layers through kvx.ops.store_kvcache on the
-    current stream and returns `next_token` for each sequence.
+    nanovllm's ModelRunner does (model_runner.py:156-166, 186) and uploads
+    it, the token ids and the positions through pinned memory without
+    blocking the host (:169-173, 187-190), writes synthetic_kv rows for all
+    layers through kvx.ops.store_kvcache on the current stream and returns
+    `next_token` for each sequence.
     """
 
     def __init__(self, pool: torch.Tensor, next_token: int = 1):
@@ -139,7 +143,7 @@ class SyntheticKVRunner:
         if method == "exit":
             return None
         from kvx import ops
-        from kvx.engine.llm_engine import decode_slot_mapping, prefill_slot_mapping
+        from kvx.engine.slot_mapping import decode_slot_mapping, prefill_slot_mapping, upload
 
         seqs, is_prefill = args
         bs = self.block_size
@@ -149,17 +153,18 @@ class SyntheticKVRunner:
             for seq in seqs:
                 start = seq.num_cached_tokens
                 toks += seq.token_ids[start:start + seq.num_scheduled_tokens]
-                pos += range(start, start + seq.num_scheduled_tokens)
+                pos.append(np.arange(start, start + seq.num_scheduled_tokens, dtype=np.int64))
+            pos = np.concatenate(pos) if pos else np.empty(0, dtype=np.int64)
         else:
             slots = decode_slot_mapping(seqs, bs)
             toks = [seq.last_token for seq in seqs]
-            pos = [len(seq) - 1 for seq in seqs]
-        if slots:
+            pos = np.array([len(seq) - 1 for seq in seqs], dtype=np.int64)
+        if len(slots):
             pool = self.kv_cache
             dev = pool.device
-            t = torch.tensor(toks, device=dev)
-            p = torch.tensor(pos, device=dev)
-            mapping = torch.tensor(slots, dtype=torch.int32, device=dev)
+            t = upload(np.asarray(toks, dtype=np.int64), dev)
+            p = upload(pos, dev)
+            mapping = upload(slots, dev)
             kv = synthetic_kv(t, p, pool.shape[1], pool.shape[4], pool.shape[5], pool.dtype)
             for layer in range(pool.shape[1]):
                 ops.store_kvcache(kv[0, layer], kv[1, layer], pool[0, layer], pool[1, layer], mapping)
