@@ -239,8 +239,9 @@ int kvx_cache_save_noalloc(kvx_cache* cache, const int32_t* block_ids_host, cons
  * marked pending until before_block_use/before_block_reuse. A block may
  * appear only once per call (KVX_E_INVALID). Calls of one or two blocks with
  * wait != 0, issued while no save is in flight, have the restore kernel read
- * the slots itself (a capped grid, system-scope loads); others are staged in
- * device memory by an H2D copy first.
+ * the slots itself (a capped grid, system-scope loads), queued on
+ * compute_stream, which waits for them anyway; others are staged in device
+ * memory by an H2D copy first, on the restore stream.
  */
 int kvx_cache_restore(kvx_cache* cache, const int32_t* slots_host, const int32_t* block_ids_host,
                       int32_t n, int32_t wait, void* compute_stream);
