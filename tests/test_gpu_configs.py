@@ -8,8 +8,8 @@ Config 3: BF16 byte-exact save of 200 scattered Qwen3-8B blocks to pinned host s
           restores only its tail.
 Config 4: ragged continuous-batch store_kvcache (16 sequences, strided V, -1 padding) over all 36 layers while FP8
           saves of 64 evicted blocks run on the save stream.
-Bit-exact checks use the oracle on a sample of blocks or layers (the C oracle is single-threaded per chunk) and
-size-independent checks (byte equality on the device) for the rest.
+Every FP8 block is checked bit-exactly against the oracle (payload, scales and the restored bytes), in chunks
+of blocks so host memory stays bounded; every BF16 block and every store_kvcache layer byte-exactly.
 """
 
 from collections import deque
@@ -59,6 +59,31 @@ def same_bytes(a: torch.Tensor, b: torch.Tensor) -> bool:
     return torch.equal(a.contiguous().view(torch.int16), b.contiguous().view(torch.int16))
 
 
+def check_fp8_entries(sources: torch.Tensor, entries: np.ndarray, restored: torch.Tensor, layout, offset: int,
+                      fp32: bool, label: str, chunk: int = 16):
+    """Every block i: entries[i] holds the oracle's codes and scales of sources[:, :, i], and restored[:, :, i]
+    the oracle's dequantisation of them (bit-exact); also the reference's acceptance bound |delta| <= amax/16.
+
+    sources/restored: [2, L, n, BS, H, hd] device tensors; entries: [n, entry_stride] uint8 host entries.
+    """
+    n = sources.shape[2]
+    rows = layout.planes * layout.plane_rows
+    sbytes = 4 if fp32 else 2
+    for lo in range(0, n, chunk):
+        hi = min(n, lo + chunk)
+        src = bf16_bits(sources[:, :, lo:hi].transpose(0, 2).transpose(1, 2))  # [blocks, 2, L, BS, H, hd]
+        got = bf16_bits(restored[:, :, lo:hi].transpose(0, 2).transpose(1, 2))
+        codes, scales = oracle.quantize(src, fp32)
+        back = oracle.dequantize(codes, scales, fp32)
+        for j, i in enumerate(range(lo, hi)):
+            assert np.array_equal(entries[i, :codes[j].size], codes[j].ravel()), f"{label}: payload of block {i}"
+            assert np.array_equal(entries[i, offset:offset + rows * sbytes], scales[j].view(np.uint8).ravel()), \
+                f"{label}: scales of block {i}"
+            assert np.array_equal(got[j], back[j]), f"{label}: restored block {i}"
+        s = sources[:, :, lo:hi].float()
+        assert torch.all((restored[:, :, lo:hi].float() - s).abs() <= s.abs().amax(-1, keepdim=True) / 16), label
+
+
 def test_config1_fp8_round_trip_of_16_blocks(gpu):
     pool = torch.empty(QWEN3_0_6B.shape, dtype=torch.bfloat16, device=gpu)
     fill_normal(pool, seed=0)
@@ -69,21 +94,14 @@ def test_config1_fp8_round_trip_of_16_blocks(gpu):
     staging = torch.empty(16 * stride, dtype=torch.uint8, device=gpu)
     entries = [staging.data_ptr() + i * stride for i in range(16)]
     source_copy = pool[:, :, sources].clone()
+    others = sorted(set(range(QWEN3_0_6B.num_blocks)) - set(dests))
+    canary = pool[:, :, others].clone()
     ops.save_blocks(pool, sources, entries, ops.FORMAT_FP8, torch.float32)
     ops.restore_blocks(pool, dests, entries, ops.FORMAT_FP8, torch.float32)
     torch.cuda.synchronize()
-    restored = pool[:, :, dests].float()
-    src = source_copy.float()
-    bound = src.abs().amax(-1, keepdim=True) / 16  # bench/test_cpu_cache_optimizations.py:71-73
-    assert torch.all((restored - src).abs() <= bound)
-    staged = u8(staging).reshape(16, stride)
-    rows = layout.planes * layout.plane_rows
-    for i in (0, 7, 15):  # bit-exact on a sample (the oracle is the slow part)
-        x = bf16_bits(source_copy[:, :, i])
-        codes, scales = oracle.quantize(x, True)
-        assert np.array_equal(staged[i, :codes.size], codes.ravel())
-        assert np.array_equal(staged[i, offset:offset + rows * 4], scales.view(np.uint8).ravel())
-        assert np.array_equal(bf16_bits(pool[:, :, dests[i]]), oracle.dequantize(codes, scales, True))
+    check_fp8_entries(source_copy, u8(staging).reshape(16, stride), pool[:, :, dests], layout, offset, True,
+                      "config 1")
+    assert same_bytes(pool[:, :, others], canary)
 
 
 @pytest.mark.parametrize("scale_dtype", [torch.float32, torch.bfloat16])
@@ -95,7 +113,6 @@ def test_config2_fp8_128_blocks_through_pinned_slots(gpu, scale_dtype):
     order = block_selection(QWEN3_8B.num_blocks, 256, seed=1)
     sources, dests = order[:128], order[128:]
     fp32 = scale_dtype == torch.float32
-    sbytes = 4 if fp32 else 2
     layout = ops.pool_layout(pool, scale_dtype)
     engine = _CopyEngine(pool, layout, ops.FORMAT_FP8, split=True)
     try:
@@ -113,27 +130,8 @@ def test_config2_fp8_128_blocks_through_pinned_slots(gpu, scale_dtype):
         engine.before_block_use(dests[0], compute)  # (all 128 share one restore event)
         engine.synchronize()
         torch.cuda.synchronize()
-        rows = layout.planes * layout.plane_rows
-        shape = source_copy[:, :, 0].shape
-        entries = slab.view(128, stride)
-        for i in range(128):
-            # Size-independent checks on the device for every block: the restore is the reference's dequantize of
-            # the host entry (fp32 code x scale, one rounding to bf16; exact product for bf16 scales), within the
-            # reference's bound.
-            entry = entries[i].to(gpu)
-            codes = entry[:rows * layout.head_dim].view(torch.float8_e4m3fn).view(shape)
-            scales = entry[offset:offset + rows * sbytes].view(scale_dtype).view(*shape[:-1], 1)
-            expect = (codes.float() * scales.float()).to(torch.bfloat16)
-            got = pool[:, :, dests[i]]
-            assert same_bytes(got, expect), f"block {sources[i]} -> {dests[i]}"
-            src = source_copy[:, :, i].float()
-            assert torch.all((got.float() - src).abs() <= src.abs().amax(-1, keepdim=True) / 16)
-        host = entries.numpy()
-        for i in (0, 63, 127):  # bit-exact against the oracle on a sample
-            codes, scales = oracle.quantize(bf16_bits(source_copy[:, :, i]), fp32)
-            assert np.array_equal(host[i, :codes.size], codes.ravel()), f"payload of block {sources[i]}"
-            assert np.array_equal(host[i, offset:offset + rows * sbytes], scales.view(np.uint8).ravel())
-            assert np.array_equal(bf16_bits(pool[:, :, dests[i]]), oracle.dequantize(codes, scales, fp32))
+        check_fp8_entries(source_copy, slab.view(128, stride).numpy(), pool[:, :, dests], layout, offset, fp32,
+                          f"config 2, {scale_dtype} scales")
         assert same_bytes(pool[:, :, others], canary)  # no block outside the destinations was written
     finally:
         engine.close()
@@ -285,9 +283,11 @@ def test_config4_ragged_store_kvcache_with_concurrent_fp8_saves(gpu):
         oracle.store_kvcache(bf16_bits(key), bf16_bits(value), expect, expect.copy(), slots)
         assert np.array_equal(bf16_bits(pool[0, layer]).reshape(-1, heads * hd), expect)
     assert torch.equal(pool[:, :, evicted], evicted_before)  # the batch never touches evicted blocks
-    host_before = bf16_bits(evicted_before)
-    for i in (0, 31, 63):
-        entry = cache._entries[keys[i]]
-        codes, scales = oracle.quantize(host_before[:, :, i], True)
-        assert np.array_equal(u8(entry.kv), codes) and np.array_equal(u8(entry.scale), scales.view(np.uint8))
+    for lo in range(0, 64, 16):  # every saved entry, bit-exact
+        codes, scales = oracle.quantize(bf16_bits(evicted_before[:, :, lo:lo + 16].transpose(0, 2).transpose(1, 2)),
+                                        True)
+        for j in range(16):
+            entry = cache._entries[keys[lo + j]]
+            assert np.array_equal(u8(entry.kv), codes[j]), f"payload of evicted block {lo + j}"
+            assert np.array_equal(u8(entry.scale), scales[j].view(np.uint8)), f"scales of evicted block {lo + j}"
     cache.close()

@@ -259,20 +259,23 @@ def test_store_kvcache_matches_the_closed_form(gpu, heads, hd):
     n, num_blocks, bs = 1000, 8, 256
     key, value = fused_qkv(n, 32, heads, hd, gpu, seed=heads)
     assert value.stride(0) == (32 + 2 * heads) * hd  # the fused QKV row stride
-    pool = torch.full((2, 1, num_blocks, bs, heads, hd), -7.0, dtype=torch.bfloat16, device=gpu)
+    pool = torch.empty((2, 1, num_blocks, bs, heads, hd), dtype=torch.bfloat16, device=gpu)
+    pool[0].fill_(-7.0)  # distinct canaries for the K and V caches
+    pool[1].fill_(-5.0)
     k_cache, v_cache = pool[0, 0], pool[1, 0]
     rng = np.random.default_rng(heads)
     slots = rng.permutation(num_blocks * bs)[:n].astype(np.int32)
     slots[rng.random(n) < 0.1] = -1  # graph padding
     slots[5] = num_blocks * bs + 3   # outside the cache: written nowhere
     mapping = torch.from_numpy(slots).to(gpu)
-    ops.store_kvcache(key, value, k_cache, v_cache, mapping)
-    k_ref, v_ref = bf16_bits(k_cache), bf16_bits(v_cache)
+    k_ref, v_ref = bf16_bits(k_cache), bf16_bits(v_cache)  # the caches before the kernel
     oracle.store_kvcache(bf16_bits(key), bf16_bits(value), k_ref, v_ref, slots)
+    ops.store_kvcache(key, value, k_cache, v_cache, mapping)
     torch.cuda.synchronize()
     assert np.array_equal(bf16_bits(k_cache), k_ref) and np.array_equal(bf16_bits(v_cache), v_ref)
-    assert (bf16_bits(pool[0, 0]) == bf16_bits(torch.tensor(-7.0, dtype=torch.bfloat16))).sum() == \
-        num_blocks * bs * heads * hd - int(((slots >= 0) & (slots < num_blocks * bs)).sum()) * heads * hd
+    untouched = num_blocks * bs * heads * hd - int(((slots >= 0) & (slots < num_blocks * bs)).sum()) * heads * hd
+    for cache, canary in ((k_cache, -7.0), (v_cache, -5.0)):
+        assert (bf16_bits(cache) == bf16_bits(torch.tensor(canary, dtype=torch.bfloat16))).sum() == untouched
 
 
 def test_store_kvcache_replays_inside_a_hip_graph(gpu):
