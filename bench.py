@@ -1,20 +1,23 @@
 #!/usr/bin/env python3
 """FP8 save + restore of Qwen3-8B-shaped KV blocks on one MI355X through libkvx.
 
-Workload: a [2, 36, 320, 256, 8, 128] bf16 pool holding 0.5 * t(df=4) values
-with 4 seeded outlier channels (x20) per (K/V, layer, KV head). One step saves
-128 seeded blocks (gather + per-(token, head) e4m3 quantisation, fp32 scales)
-into HBM-resident entries and restores those entries into 128 other seeded
-blocks (dequantisation + scatter): one launch each, inputs resident in HBM.
+Workload (config 2): a [2, 36, 320, 256, 8, 128] bf16 pool holding
+0.5 * t(df=4) values with 4 seeded outlier channels (x20) per (K/V, layer,
+KV head). One step saves 128 seeded blocks into pinned host slab slots
+(gather + per-(token, head) e4m3 quantisation into device staging, then
+DMA; fp32 scales) on the save stream while 128 host entries are restored
+into 128 other seeded blocks (DMA into staging, then dequantisation +
+scatter) on the restore stream: the two directions of the host link overlap.
 
-`value` is logical KV throughput: BF16-equivalent bytes saved + restored per
-second (37,748,736 B per block and direction). `roofline` prices the
-dominant kernel's algorithmic HBM bytes (57,212,928 B per block: 36 MiB bf16
-read, 18 MiB e4m3 + 576 KiB fp32 scales written, or the reverse) per launch
-against 8 TB/s, timed with HIP events on its stream. `host_link` reports the
-same blocks moved to and from pinned host slabs through the copy engine
-(PCIe-inclusive; not `value`). `cpu_baseline` times the reference's CPU path
-(its torch codec on CPU tensors) on a bounded sample of the same blocks.
+`value` is logical KV throughput of that step: BF16-equivalent bytes saved +
+restored per second (37,748,736 B per block and direction). `host_link`
+prices the step's entry bytes against the PCIe link (spec and a measured
+pinned-memcpy ceiling). `roofline` prices the dominant kernel's algorithmic
+HBM bytes (57,212,928 B per block: 36 MiB bf16 read, 18 MiB e4m3 + 576 KiB
+fp32 scales written, or the reverse) per launch against 8 TB/s, timed with
+HIP events on its stream in the same save + restore with entries in HBM
+(`kernels`). `cpu_baseline` times the reference's CPU path (its torch codec
+on CPU tensors) on a bounded sample of the same blocks.
 
 Run: python bench.py [--steps 50] [--warmup 5] [--blocks 128]
 """
@@ -25,6 +28,7 @@ import json
 import os
 import sys
 import time
+from contextlib import contextmanager
 from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
@@ -41,6 +45,23 @@ def log(*args):
     print(*args, file=sys.stderr, flush=True)
 
 
+@contextmanager
+def marked(name: str):
+    """A named range in rocprofv3's marker trace (roctx, through torch.cuda.nvtx), to split traces by leg."""
+    import torch
+
+    try:
+        torch.cuda.nvtx.range_push(name)
+        pushed = True
+    except Exception:  # no marker library: the range is only a label
+        pushed = False
+    try:
+        yield
+    finally:
+        if pushed:
+            torch.cuda.nvtx.range_pop()
+
+
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
@@ -49,6 +70,9 @@ def parse_args():
     p.add_argument("--blocks", type=int, default=128, help="blocks saved and restored per step")
     p.add_argument("--scale", choices=("fp32", "bf16"), default="fp32")
     p.add_argument("--skip-host-link", action="store_true")
+    p.add_argument("--skip-sdma-probe", action="store_true",
+                   help="skip the host-link probe that queues HSA copies on explicit SDMA engines (it crashed the "
+                        "process under rocprofv3's memory-copy tracing, which intercepts those calls)")
     p.add_argument("--skip-cpu-baseline", action="store_true")
     p.add_argument("--skip-store", action="store_true", help="skip the store_kvcache leg")
     p.add_argument("--skip-store-concurrency", action="store_true",
@@ -61,7 +85,6 @@ def parse_args():
                    help="skip timing the reference's torch codec chain on the GPU")
     p.add_argument("--skip-configs", action="store_true",
                    help="skip the Qwen3-0.6B FP8 and Qwen3-8B BF16 legs")
-    p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample budget")
     p.add_argument("--host-reps", type=int, default=3)
     p.add_argument("--calibrate-copy", action="store_true",
                    help="after timing, gather the same blocks once with the BF16 copy kernel (known bytes), "
@@ -186,6 +209,14 @@ def store_leg(torch, ops, pool, reps=5, concurrency=True):
     out["paged_blocks"] = {"tokens": pos, "ms_all_layers": round(1000 * t, 4),
                            "algorithmic_bytes_per_launch": per_launch, "hbm_gbs": round(gbs, 1),
                            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    # The same kernel and batch with the destinations in slot order (a prefill into fresh, consecutive blocks):
+    # the rate the kernel reaches when its writes stream, against which the random 2 KiB rows are priced.
+    contiguous = np.full(padded, -1, dtype=np.int32)
+    contiguous[:total] = np.arange(total, dtype=np.int32)
+    t, per_launch, gbs = timed(contiguous, total)
+    out["contiguous_slots"] = {"tokens": total, "ms_all_layers": round(1000 * t, 4), "hbm_gbs": round(gbs, 1),
+                               "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    out["random_vs_contiguous"] = round(out["hbm_gbs"] / gbs, 4)
     if concurrency:
         out["with_concurrent_saves"] = store_beside_saves(torch, ops, pool, key, value, lengths, reps)
     return out
@@ -361,11 +392,13 @@ def microbench_leg(torch, blocks=64, matmul_iters=200):
         res = {"slab_preallocate_s": round(time.perf_counter() - start, 3)}
         entry = cache.block_bytes
         try:
-            res["slab_save"] = per_block(*timed(lambda: [cache.save_block(h) for h in hashes]), entry)
+            with marked(f"microbench {name}: slab saves"):
+                res["slab_save"] = per_block(*timed(lambda: [cache.save_block(h) for h in hashes]), entry)
             for h in hashes:
                 block = manager.blocks[manager.hash_to_block_id.pop(h)]
                 block.hash, block.token_ids = -1, []
-            res["slab_restore"] = per_block(*timed(lambda: [cache.restore_block(h) for h in hashes]), entry)
+            with marked(f"microbench {name}: slab restores"):
+                res["slab_restore"] = per_block(*timed(lambda: [cache.restore_block(h) for h in hashes]), entry)
         finally:
             cache.close()
         manager, hashes = published()
@@ -460,14 +493,16 @@ def agent_leg(torch, pool, scale_dtype):
         if not batched:
             cache.coalesce = nullcontext  # the block manager then issues one engine call per block
         try:
-            r = run_agent_pressure(engine, agents=4, context=32768, turns=turns, append=2048, verify=False)
+            with marked(f"agents: {name}"):
+                r = run_agent_pressure(engine, agents=4, context=32768, turns=turns, append=2048, verify=False)
         finally:
             engine.exit()
         if name == "warm-up":
             continue
         out[name] = {"wall_s": round(r.wall_s, 3), "saved_blocks": r.saved_blocks,
                      "restored_blocks": r.restored_blocks, "prefetched_blocks": r.prefetched_blocks,
-                     "d2h_bytes": r.d2h_bytes, "h2d_bytes": r.h2d_bytes, "link_gbs": round(r.link_gbs, 2)}
+                     "d2h_bytes": r.d2h_bytes, "h2d_bytes": r.h2d_bytes, "link_gbs": round(r.link_gbs, 2),
+                     "host_blocked_s": round(r.host_blocked_s, 3), "drain_s": round(r.drain_s, 4)}
     out["split_speedup"] = round(out["one_copy_stream"]["wall_s"] / out["split_streams"]["wall_s"], 3)
     out["batching_speedup"] = round(out["per_block_calls"]["wall_s"] / out["split_streams"]["wall_s"], 3)
     return out
@@ -591,12 +626,15 @@ def reference_link_leg(torch, pool, sources, dests, scale_dtype, reps=3):
 
 
 def handoff_leg(torch, pool, reps=3):
-    """KV handoff of one 32,767-token request (128 blocks) on the Qwen3-8B pool: export and import.
+    """KV handoff of one 32,767-token request (128 blocks) on the Qwen3-8B pool: export and import, BF16 and FP8.
 
-    kvx: kv_handoff.export_kv / import_kv's copies (the token gather writes a
-    pinned host payload; the scatter reads it in place). Beside them, the
-    reference's copies for the same request on this GPU (kv_handoff.py:46-55:
-    index_select, pack, .cpu(); :112-118: .to(device), one copy_ per block).
+    kvx: export_kv's copy (the token gather writes the pinned host payload,
+    quantising it for FP8) and import_kv's (one host-to-device DMA per tensor,
+    then the token scatter, dequantising for FP8), each waited for. Beside
+    them, the reference's BF16 copies for the same request on this GPU
+    (kv_handoff.py:46-55: index_select, pack, .cpu(); :112-118: .to(device),
+    one copy_ per block). `wire_gbs` counts payload bytes (what crosses the
+    link), `logical_kv_gbs` the BF16 bytes of the request's KV.
     """
     from kvx import ops
     from workloads import block_selection
@@ -606,8 +644,9 @@ def handoff_leg(torch, pool, reps=3):
     table = block_selection(nb, 128, seed=1)
     dest = block_selection(nb, 128, seed=2)
     shape = (2, layers, count, heads, hd)
-    nbytes = 2 * layers * count * heads * hd * pool.element_size()
-    stream = torch.cuda.current_stream(pool.device)
+    logical = 2 * layers * count * heads * hd * pool.element_size()
+    device = pool.device
+    stream = torch.cuda.current_stream(device)
 
     def timed(fn):
         best = None
@@ -620,33 +659,49 @@ def handoff_leg(torch, pool, reps=3):
             best = dt if best is None else min(best, dt)
         return best
 
-    snapshot = torch.empty(shape, dtype=pool.dtype, pin_memory=True)
+    bf16 = torch.empty(shape, dtype=pool.dtype, pin_memory=True)
+    codes = torch.empty(shape, dtype=torch.float8_e4m3fn, pin_memory=True)
+    scales = torch.empty((*shape[:-1], 1), dtype=torch.float32, pin_memory=True)
+    fp8_bytes = codes.numel() + scales.numel() * scales.element_size()
 
     def kvx_export():
-        ops.gather_tokens(pool, table, count, snapshot)
+        ops.gather_tokens(pool, table, count, bf16)
         stream.synchronize()
 
     def kvx_import():
-        ops.scatter_tokens(pool, dest, count, snapshot)
+        ops.scatter_tokens(pool, dest, count, bf16.to(device, non_blocking=True))
+        stream.synchronize()
 
-    ids = torch.tensor(table, dtype=torch.int64, device=pool.device)
+    def kvx_export_fp8():
+        ops.gather_tokens_fp8(pool, table, count, codes, scales)
+        stream.synchronize()
+
+    def kvx_import_fp8():
+        ops.scatter_tokens_fp8(pool, dest, count, codes.to(device, non_blocking=True),
+                               scales.to(device, non_blocking=True))
+        stream.synchronize()
+
+    ids = torch.tensor(table, dtype=torch.int64, device=device)
     held = {}
 
     def reference_export():
         held["kv"] = pool.index_select(2, ids).flatten(2, 3)[:, :, :count].contiguous().cpu()
 
     def reference_import():
-        payload = held["kv"].to(device=pool.device)
-        for logical, physical in enumerate(dest):
-            start = logical * bs
+        payload = held["kv"].to(device=device)
+        for logical_block, physical in enumerate(dest):
+            start = logical_block * bs
             end = min(start + bs, count)
             pool[:, :, physical, :end - start].copy_(payload[:, :, start:end])
 
-    out = {"tokens": count, "bytes": nbytes}
-    for name, fn in (("kvx_export", kvx_export), ("kvx_import", kvx_import),
-                     ("reference_export", reference_export), ("reference_import", reference_import)):
+    out = {"tokens": count, "bf16_payload_bytes": logical, "fp8_payload_bytes": fp8_bytes}
+    for name, fn, wire in (("kvx_export", kvx_export, logical), ("kvx_import", kvx_import, logical),
+                           ("kvx_export_fp8", kvx_export_fp8, fp8_bytes), ("kvx_import_fp8", kvx_import_fp8, fp8_bytes),
+                           ("reference_export", reference_export, logical),
+                           ("reference_import", reference_import, logical)):
         seconds = timed(fn)
-        out[name] = {"ms": round(1000 * seconds, 2), "gbs": round(nbytes / seconds / 1e9, 2)}
+        out[name] = {"ms": round(1000 * seconds, 2), "wire_gbs": round(wire / seconds / 1e9, 2),
+                     "logical_kv_gbs": round(logical / seconds / 1e9, 2)}
     return out
 
 
@@ -721,28 +776,29 @@ def host_link_leg(torch, pool, layout, sources, dests, reps, fmt=None, ceilings=
         compute = torch.cuda.current_stream(pool.device).cuda_stream
         low, high = list(range(n)), list(range(n, 2 * n))
 
-        def timed(fn):
+        def timed(fn, label="host link"):
             best = None
-            for _ in range(reps):
-                torch.cuda.synchronize()
-                t0 = time.perf_counter()
-                fn()
-                engine.synchronize()
-                torch.cuda.synchronize()
-                dt = time.perf_counter() - t0
-                best = dt if best is None else min(best, dt)
+            with marked(label):
+                for _ in range(reps):
+                    torch.cuda.synchronize()
+                    t0 = time.perf_counter()
+                    fn()
+                    engine.synchronize()
+                    torch.cuda.synchronize()
+                    dt = time.perf_counter() - t0
+                    best = dt if best is None else min(best, dt)
             return best
 
         engine.save(sources, low, compute)  # fill the restore source slots
         engine.synchronize()
-        save_s = timed(lambda: engine.save(sources, high, compute))
-        restore_s = timed(lambda: engine.restore(low, dests, False, compute))
+        save_s = timed(lambda: engine.save(sources, high, compute), "host link: saves alone")
+        restore_s = timed(lambda: engine.restore(low, dests, False, compute), "host link: restores alone")
 
         def both():
             engine.save(sources, high, compute)
             engine.restore(low, dests, False, compute)
 
-        both_s = timed(both)
+        both_s = timed(both, "host link: both")
 
         # What CPUBlockCache does: one engine call per block, with its default staging.
         from kvx.engine.cpu_prefix_cache import _MAX_BATCH, _STAGING_BYTES
@@ -763,7 +819,9 @@ def host_link_leg(torch, pool, layout, sources, dests, reps, fmt=None, ceilings=
                     engine.save(sources[i:i + k], high[i:i + k], compute)
                     engine.restore(low[i:i + k], dests[i:i + k], False, compute)
 
-            save_s_k, restore_s_k, both_s_k = timed(save_each), timed(restore_each), timed(both_each)
+            save_s_k = timed(save_each, f"host link: saves, calls of {k}")
+            restore_s_k = timed(restore_each, f"host link: restores, calls of {k}")
+            both_s_k = timed(both_each, f"host link: both, calls of {k}")
             return {"save_d2h_gbs": round(gbs(link_bytes, save_s_k), 2),
                     "restore_h2d_gbs": round(gbs(link_bytes, restore_s_k), 2),
                     "duplex_gbs": round(gbs(2 * link_bytes, both_s_k), 2)}
@@ -805,9 +863,9 @@ def host_link_leg(torch, pool, layout, sources, dests, reps, fmt=None, ceilings=
                     assert hip.hipMemcpyAsync(flat_dev2.data_ptr() + off, host_b + off, size, 1, s2) == 0
 
             piece_sizes = (8 << 20, 16 << 20, 32 << 20, 64 << 20, -(-link_bytes // 16))
-            ceil_d2h = min(timed(lambda: d2h(p)) for p in piece_sizes)
-            ceil_h2d = min(timed(lambda: h2d(p)) for p in piece_sizes)
-            ceil_both = min(timed(lambda: both_ways(p)) for p in piece_sizes)
+            ceil_d2h = min(timed(lambda: d2h(p), f"memcpy d2h, {p} B pieces") for p in piece_sizes)
+            ceil_h2d = min(timed(lambda: h2d(p), f"memcpy h2d, {p} B pieces") for p in piece_sizes)
+            ceil_both = min(timed(lambda: both_ways(p), f"memcpy both, {p} B pieces") for p in piece_sizes)
         overlap = (save_s + restore_s - both_s) / min(save_s, restore_s)
         duplex = gbs(2 * link_bytes, both_s)
         out = {
@@ -836,49 +894,369 @@ def host_link_leg(torch, pool, layout, sources, dests, reps, fmt=None, ceilings=
         engine.close()
 
 
-def cpu_baseline_leg(torch, shape, scale_dtype, seconds):
-    """The reference's CPU path (its torch codec on CPU tensors) on Qwen3-8B blocks."""
+def gpu_pci_address(device_index: int = 0):
+    """The GPU's PCI address ("0000:xx:yy.z") as the HIP runtime torch loaded reports it."""
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    buf = ctypes.create_string_buffer(64)
+    hip.hipDeviceGetPCIBusId.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_int]
+    if hip.hipDeviceGetPCIBusId(buf, 64, device_index) != 0:
+        return None
+    return buf.value.decode().lower()
+
+
+def pcie_path(bdf):
+    """Negotiated and maximum link speed/width of the GPU's PCI function and every bridge above it (sysfs)."""
+    import re
+
+    if bdf is None:
+        return []
+    path = os.path.realpath(f"/sys/bus/pci/devices/{bdf}")
+    hops = []
+    while re.fullmatch(r"[0-9a-f]{4}:[0-9a-f]{2}:[0-9a-f]{2}\.[0-7]", os.path.basename(path)):
+        hop = {"bdf": os.path.basename(path)}
+        for key in ("current_link_speed", "current_link_width", "max_link_speed", "max_link_width"):
+            try:
+                hop[key] = Path(path, key).read_text().strip()
+            except OSError:
+                hop[key] = None
+        hops.append(hop)
+        path = os.path.dirname(path)
+    return hops
+
+
+def host_inventory(torch):
+    """What the CPU baseline and the host link run on (the reference records the same: bench/inventory.py:79-105)."""
+    affinity = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        limit, period = Path("/sys/fs/cgroup/cpu.max").read_text().split()
+        if limit != "max":
+            quota = int(limit) / int(period)
+    except (OSError, ValueError):
+        pass
+    model = None
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    usable = affinity if quota is None else max(1, min(affinity, int(quota)))
+    bdf = gpu_pci_address(0)
+    return {"nproc": os.cpu_count(), "affinity_cpus": affinity, "cgroup_cpu_quota": quota, "cpu_model": model,
+            "usable_cpus": usable, "torch_threads_default": torch.get_num_threads(),
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS"), "gpu": torch.cuda.get_device_name(0),
+            "gpu_pci": bdf, "pcie_path": pcie_path(bdf)}
+
+
+def headline_leg(torch, pool, layout, sources, dests, steps, warmup):
+    """Config 2 end to end: each step saves the sources into pinned host slots and restores as many host entries
+    into the destinations, overlapped on the copy engine's save and restore streams (the C ABI calls the cache
+    makes: one kvx_cache_save and one kvx_cache_restore of 128 blocks)."""
+    from kvx import ops
+    from kvx.engine.cpu_prefix_cache import _CopyEngine
+
+    n = len(sources)
+    engine = _CopyEngine(pool, layout, ops.FORMAT_FP8, split=True)
+    try:
+        stride = engine.entry_stride
+        slab = torch.empty(2 * n * stride, dtype=torch.uint8, pin_memory=True)
+        staging = [torch.empty(n * stride, dtype=torch.uint8, device=pool.device) for _ in range(2)]
+        engine.add_slab(slab, 2 * n)
+        engine.set_staging(*staging, n)
+        compute = torch.cuda.current_stream(pool.device).cuda_stream
+        restored_slots, saved_slots = list(range(n)), list(range(n, 2 * n))
+        engine.save(sources, restored_slots, compute)  # the host entries the steps restore
+        engine.synchronize()
+
+        def step():
+            engine.save(sources, saved_slots, compute)
+            engine.restore(restored_slots, dests, False, compute)
+
+        for _ in range(warmup):
+            step()
+        engine.synchronize()
+        torch.cuda.synchronize()
+        with marked("headline: timed steps"):
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                step()
+            engine.synchronize()
+            torch.cuda.synchronize()
+            elapsed = time.perf_counter() - t0
+        return {"elapsed": elapsed, "link_bytes_per_step": 2 * n * engine.logical_bytes,
+                "streams_concurrent": engine.streams_concurrent}
+    finally:
+        engine.close()
+
+
+class SdmaCopier:
+    """Copies between a device buffer and pinned host memory on explicitly chosen SDMA engines, through HSA's
+    hsa_amd_memory_async_copy_on_engine, bypassing the HIP runtime's choice of engine (it runs device-to-host
+    hipMemcpyAsync copies as blit kernels). `unavailable` names why it cannot run on this machine, if it cannot."""
+
+    def __init__(self, torch, nbytes, piece=64 << 20):
+        import re
+
+        self.unavailable = None
+        self.nbytes, self.piece = nbytes, piece
+        try:
+            hsa = ctypes.CDLL("libhsa-runtime64.so.1")
+        except OSError as error:
+            self.unavailable = f"libhsa-runtime64 not loadable: {error}"
+            return
+        u64, u32 = ctypes.c_uint64, ctypes.c_uint32
+        hsa.hsa_init.restype = ctypes.c_int
+        hsa.hsa_iterate_agents.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        hsa.hsa_agent_get_info.argtypes = [u64, ctypes.c_int, ctypes.c_void_p]
+        hsa.hsa_signal_create.argtypes = [ctypes.c_int64, u32, ctypes.c_void_p, ctypes.POINTER(u64)]
+        hsa.hsa_signal_destroy.argtypes = [u64]
+        hsa.hsa_signal_load_scacquire.argtypes = [u64]
+        hsa.hsa_signal_load_scacquire.restype = ctypes.c_int64
+        hsa.hsa_amd_memory_copy_engine_status.argtypes = [u64, u64, ctypes.POINTER(u32)]
+        hsa.hsa_amd_memory_async_copy_on_engine.argtypes = [ctypes.c_void_p, u64, ctypes.c_void_p, u64,
+                                                            ctypes.c_size_t, u32, ctypes.c_void_p, u64, ctypes.c_int,
+                                                            ctypes.c_bool]
+        if hsa.hsa_init() != 0:
+            self.unavailable = "hsa_init failed"
+            return
+        self.hsa = hsa
+        HSA_AGENT_INFO_DEVICE, HSA_AMD_AGENT_INFO_BDFID = 17, 0xA006
+        agents = {"cpu": [], "gpu": []}
+        callback_type = ctypes.CFUNCTYPE(ctypes.c_int, u64, ctypes.c_void_p)
+
+        def visit(agent, _):
+            kind = u32()
+            hsa.hsa_agent_get_info(agent, HSA_AGENT_INFO_DEVICE, ctypes.byref(kind))
+            if kind.value == 0:
+                agents["cpu"].append(agent)
+            elif kind.value == 1:
+                bdf = u32()
+                hsa.hsa_agent_get_info(agent, HSA_AMD_AGENT_INFO_BDFID, ctypes.byref(bdf))
+                agents["gpu"].append((agent, bdf.value))
+            return 0
+
+        callback = callback_type(visit)
+        hsa.hsa_iterate_agents(ctypes.cast(callback, ctypes.c_void_p), None)
+        address = gpu_pci_address(0)
+        m = re.fullmatch(r"[0-9a-f]{4}:([0-9a-f]{2}):([0-9a-f]{2})\.([0-7])", address or "")
+        want = (int(m.group(1), 16) << 8) | (int(m.group(2), 16) << 3) | int(m.group(3)) if m else None
+        gpu = next((a for a, bdf in agents["gpu"] if bdf == want), None)
+        if gpu is None and len(agents["gpu"]) == 1:
+            gpu = agents["gpu"][0][0]  # the only GPU this process sees
+        if gpu is None or not agents["cpu"]:
+            self.unavailable = f"no HSA agent matches the GPU at {address} ({len(agents['gpu'])} GPU agents)"
+            return
+        self.cpu, self.gpu = agents["cpu"][0], gpu
+        self.masks = {}
+        for name, (dst, src) in {"d2h": (self.cpu, gpu), "h2d": (gpu, self.cpu)}.items():
+            mask = u32()
+            status = hsa.hsa_amd_memory_copy_engine_status(dst, src, ctypes.byref(mask))
+            self.masks[name] = mask.value if status == 0 else 0
+        engines = {name: [1 << i for i in range(16) if mask & (1 << i)] for name, mask in self.masks.items()}
+        self.engines = {"d2h": engines["d2h"][:2]}
+        self.engines["h2d"] = [e for e in engines["h2d"] if e not in self.engines["d2h"]][:2]
+        if not self.engines["d2h"] or not self.engines["h2d"]:
+            self.unavailable = f"not enough distinct SDMA engines (masks {self.masks})"
+            return
+        self.dev_src = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+        self.dev_dst = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+        self.host_dst = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+        self.host_src = torch.zeros(nbytes, dtype=torch.uint8, pin_memory=True)
+        torch.cuda.synchronize()
+        self.pieces = [(off, min(piece, nbytes - off)) for off in range(0, nbytes, piece)]
+
+    def start(self, directions, spread=1):
+        """Queues every piece of each direction ("d2h", "h2d"), alternating over `spread` engines per direction;
+        returns the completion signals."""
+        hsa, signals = self.hsa, []
+        for direction in directions:
+            sig = ctypes.c_uint64()
+            if hsa.hsa_signal_create(len(self.pieces), 0, None, ctypes.byref(sig)) != 0:
+                raise RuntimeError("hsa_signal_create failed")
+            signals.append(sig.value)
+            engines = self.engines[direction][:spread]
+            for i, (off, size) in enumerate(self.pieces):
+                engine = engines[i % len(engines)]
+                if direction == "d2h":
+                    rc = hsa.hsa_amd_memory_async_copy_on_engine(self.host_dst.data_ptr() + off, self.cpu,
+                                                                 self.dev_src.data_ptr() + off, self.gpu, size, 0,
+                                                                 None, sig.value, engine, True)
+                else:
+                    rc = hsa.hsa_amd_memory_async_copy_on_engine(self.dev_dst.data_ptr() + off, self.gpu,
+                                                                 self.host_src.data_ptr() + off, self.cpu, size, 0,
+                                                                 None, sig.value, engine, True)
+                if rc != 0:
+                    raise RuntimeError(f"hsa_amd_memory_async_copy_on_engine ({direction}) returned {rc}")
+        return signals
+
+    def wait(self, signals, limit_s=30.0):
+        deadline = time.perf_counter() + limit_s
+        while any(self.hsa.hsa_signal_load_scacquire(sig) > 0 for sig in signals):
+            if time.perf_counter() > deadline:
+                raise RuntimeError(f"SDMA copies did not finish within {limit_s} s")
+            time.sleep(20e-6)
+        for sig in signals:
+            self.hsa.hsa_signal_destroy(sig)
+
+    def run(self, directions, spread=1):
+        t0 = time.perf_counter()
+        self.wait(self.start(directions, spread))
+        return time.perf_counter() - t0
+
+
+def sdma_probe(torch, nbytes, reps=3):
+    """Plain DMA duplex over the host link on explicit SDMA engines: D2H alone, H2D alone, both at once, each on
+    one engine and spread over two. GB/s, or why it could not run."""
+    copier = SdmaCopier(torch, nbytes)
+    if copier.unavailable:
+        return {"skipped": copier.unavailable}
+    out = {"bytes_per_direction": nbytes, "piece_bytes": copier.piece, "engines": copier.engines,
+           "engine_masks": copier.masks}
+    try:
+        for name, directions, spread in (("d2h", ["d2h"], 1), ("h2d", ["h2d"], 1), ("duplex", ["d2h", "h2d"], 1),
+                                         ("d2h_2_engines", ["d2h"], 2), ("h2d_2_engines", ["h2d"], 2),
+                                         ("duplex_2_engines_each", ["d2h", "h2d"], 2)):
+            best = min(copier.run(directions, spread) for _ in range(reps))
+            out[f"{name}_gbs"] = round(len(directions) * nbytes / best / 1e9, 2)
+    except RuntimeError as error:
+        out["error"] = str(error)
+    return out
+
+
+def interference_leg(torch, nbytes=1 << 30, reps=20, kvx_kernels=None):
+    """How a host-link copy slows HBM-bound kernels on another stream.
+
+    The kernels: `reps` elementwise adds over 512 MiB of bf16 (torch), and
+    each of `kvx_kernels` ({name: callable queuing kvx work on the current
+    stream}), on a stream checked to run beside the copy stream. Each runs
+    alone, then beside 1 GiB moved by the runtime's device-to-host
+    hipMemcpyAsync (which it runs as blit kernels), its host-to-device copy
+    (DMA), and an SDMA-engine device-to-host copy queued through HSA.
+    """
+    from kvx.engine.cpu_prefix_cache import _copy_streams
+
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    hip.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
+    (copy_stream, work_stream), concurrent = _copy_streams(torch.device("cuda", 0), 2)
+    dev = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    host = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+    a = torch.randn(1 << 28, device="cuda").to(torch.bfloat16)
+    b = torch.empty_like(a)
+    piece = 64 << 20
+    copier = SdmaCopier(torch, nbytes)
+
+    def adds():
+        for _ in range(reps):
+            torch.add(a, 1, out=b)
+
+    def kernels_ms(start=None, finish=None, work=adds):
+        torch.cuda.synchronize()
+        handle = start() if start else None
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(work_stream):
+            e0.record(work_stream)
+            work()
+            e1.record(work_stream)
+        if finish:
+            finish(handle)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1)
+
+    def runtime_copy(kind):
+        def start():
+            for off in range(0, nbytes, piece):
+                dst, src = (host, dev) if kind == 2 else (dev, host)
+                assert hip.hipMemcpyAsync(dst.data_ptr() + off, src.data_ptr() + off, piece, kind,
+                                          copy_stream.cuda_stream) == 0
+        return start
+
+    out = {"streams_concurrent": concurrent, "copy_bytes": nbytes,
+           "sdma": copier.unavailable or "available"}
+    for name, work in {f"{reps} x torch.add over 512 MiB bf16": adds, **(kvx_kernels or {})}.items():
+        kernels_ms(work=work)
+        res = {"alone_ms": round(kernels_ms(work=work), 3)}
+        with marked(f"interference: {name} beside runtime D2H"):
+            res["beside_runtime_d2h_ms"] = round(kernels_ms(runtime_copy(2), work=work), 3)
+        with marked(f"interference: {name} beside runtime H2D"):
+            res["beside_runtime_h2d_ms"] = round(kernels_ms(runtime_copy(1), work=work), 3)
+        if not copier.unavailable:
+            with marked(f"interference: {name} beside SDMA D2H"):
+                res["beside_sdma_d2h_ms"] = round(kernels_ms(lambda: copier.start(["d2h"]), copier.wait, work), 3)
+        out[name] = res
+    return out
+
+
+def cpu_baseline_leg(torch, pool, sources, dests, scale_dtype, inventory, pairs=48, runs=5):
+    """The reference's CPU path on this host: its torch codec and byte copies on CPU tensors, the branches
+    CPUBlockCache takes for a CPU pool (cpu_prefix_cache.py:20-28, 323-326, 394-397).
+
+    Threads: the CPUs the process may run on at once (affinity, capped by the
+    cgroup quota). Each measurement is 1 warm-up and the median of `runs`
+    runs (time.perf_counter). Samples: `pairs` of the Qwen3-8B workload's
+    Student-t blocks (copied from the GPU pool) saved to FP8 and restored into
+    other blocks, the same `pairs` in BF16 mode, and config 1's 16 Qwen3-0.6B
+    N(0, 1) blocks.
+    """
     from oracle import torch_path
 
-    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    threads = inventory["usable_cpus"]
     torch.set_num_threads(threads)
-    cpu_blocks = 4
-    g = torch.Generator().manual_seed(0)
-    pool = (torch.randn((2, shape[1], cpu_blocks, *shape[3:]), generator=g) * 0.5).to(torch.bfloat16)
-    block_shape = (2, shape[1], *shape[3:])
-    payload = torch.empty(block_shape, dtype=torch.float8_e4m3fn)
-    scale = torch.empty((*block_shape[:-1], 1), dtype=scale_dtype)
-    torch_path.save_block(pool, 0, payload, scale)  # warm-up
-    moved, t0 = 0, time.perf_counter()
-    while True:
-        b = moved // 2 % cpu_blocks
-        torch_path.save_block(pool, b, payload, scale)
-        torch_path.restore_block(pool, (b + 1) % cpu_blocks, payload, scale)
-        moved += 2
-        elapsed = time.perf_counter() - t0
-        if elapsed >= seconds:
-            break
-    # The 16-block Qwen3-0.6B round trip (its CPU-runnable configuration), for comparison with the GPU leg.
-    small = (2, 28, 32, 256, 8, 128)
-    small_pool = torch.randn(small, generator=g).to(torch.bfloat16)
-    small_block = (2, 28, 256, 8, 128)
-    small_payload = torch.empty(small_block, dtype=torch.float8_e4m3fn)
-    small_scale = torch.empty((*small_block[:-1], 1), dtype=scale_dtype)
-    t1 = time.perf_counter()
-    for b in range(16):
-        torch_path.save_block(small_pool, b, small_payload, small_scale)
-        torch_path.restore_block(small_pool, 16 + b, small_payload, small_scale)
-    small_s = time.perf_counter() - t1
-    small_bytes = 2 * 16 * small_pool[:, :, 0].numel() * 2
+    _, layers, _, bs, heads, hd = pool.shape
+
+    def median_s(fn):
+        fn()
+        times = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        return sorted(times)[runs // 2]
+
+    def codec(host, n, fmt_scale):
+        entry = (n, 2, host.shape[1], *host.shape[3:])
+        payload = torch.empty(entry, dtype=torch.float8_e4m3fn if fmt_scale else host.dtype)
+        scale = torch.empty((*entry[:-1], 1), dtype=fmt_scale) if fmt_scale else None
+
+        def save():
+            for i in range(n):
+                torch_path.save_block(host, i, payload[i], None if scale is None else scale[i])
+
+        def restore():
+            for i in range(n):
+                torch_path.restore_block(host, n + i, payload[i], None if scale is None else scale[i])
+
+        return median_s(save), median_s(restore)
+
+    host = torch.empty((2, layers, 2 * pairs, bs, heads, hd), dtype=pool.dtype)
+    host[:, :, :pairs] = pool[:, :, sources[:pairs]].cpu()
+    fp8_save, fp8_restore = codec(host, pairs, scale_dtype)
+    raw_save, raw_restore = codec(host, pairs, None)
+    del host
+    small = torch.randn((2, 28, 32, 256, 8, 128), generator=torch.Generator(device="cuda").manual_seed(0),
+                        device="cuda").to(torch.bfloat16).cpu()
+    c1_save, c1_restore = codec(small, 16, torch.float32)
+    small_block = small[:, :, 0].numel() * 2
+    logical = lambda n, per, s: round(n * per / s / 1e9, 3)  # noqa: E731
+    value = logical(2 * pairs, BF16_BLOCK_BYTES, fp8_save + fp8_restore)
     return {
-        "qwen3_0_6b_16_blocks": {"seconds": round(small_s, 3),
-                                 "logical_kv_gbs": round(small_bytes / small_s / 1e9, 3)},
-        "value": round(moved * BF16_BLOCK_BYTES / elapsed / 1e9, 3),
+        "value": value,
         "unit": "GB/s",
-        "cores": torch.get_num_threads(),
+        "cores": threads,
         "kind": "port",
-        "sample": f"{moved // 2} save+restore pairs of Qwen3-8B blocks (FP8, {str(scale_dtype)[6:]} scales) "
-                  f"through torch's CPU codec (cpu_prefix_cache.py:20-28, 323-326, 394-397), {elapsed:.1f} s",
+        "sample": f"{pairs} Qwen3-8B blocks of the bench's pool saved to FP8 ({str(scale_dtype)[6:]} scales) and "
+                  f"restored into {pairs} others through torch's CPU codec (cpu_prefix_cache.py:20-28, 323-326, "
+                  f"394-397); median of {runs} runs after a warm-up, save and restore timed separately",
+        "fp8_qwen3_8b": {"blocks": pairs, "save_s": round(fp8_save, 4), "restore_s": round(fp8_restore, 4),
+                         "save_gbs": logical(pairs, BF16_BLOCK_BYTES, fp8_save),
+                         "restore_gbs": logical(pairs, BF16_BLOCK_BYTES, fp8_restore)},
+        "bf16_qwen3_8b": {"blocks": pairs, "save_s": round(raw_save, 4), "restore_s": round(raw_restore, 4),
+                          "save_gbs": logical(pairs, BF16_BLOCK_BYTES, raw_save),
+                          "restore_gbs": logical(pairs, BF16_BLOCK_BYTES, raw_restore)},
+        "fp8_qwen3_0_6b_16_blocks": {"save_s": round(c1_save, 4), "restore_s": round(c1_restore, 4),
+                                     "logical_kv_gbs": logical(32, small_block, c1_save + c1_restore)},
+        "threads_basis": "sched_getaffinity capped by the cgroup CPU quota",
     }
 
 
@@ -900,16 +1278,25 @@ def main():
     device = torch.device("cuda", 0)
     scale_dtype = torch.float32 if args.scale == "fp32" else torch.bfloat16
     shape = QWEN3_8B.shape
-    log(f"pool {shape} bf16 on {torch.cuda.get_device_name(device)}")
+    inventory = host_inventory(torch)
+    log(f"pool {shape} bf16 on {inventory['gpu']} at {inventory['gpu_pci']}; {inventory['usable_cpus']} usable CPUs")
+    log(f"PCIe path: {json.dumps(inventory['pcie_path'])}")
     pool = torch.empty(shape, dtype=torch.bfloat16, device=device)
     fill_student_t(pool, seed=0)
     torch.cuda.synchronize()
     order = block_selection(QWEN3_8B.num_blocks, 2 * args.blocks, seed=1)
     sources, dests = order[:args.blocks], order[args.blocks:]
+    layout = ops.pool_layout(pool, scale_dtype)
+    n = args.blocks
+
+    log("config 2: saves to and restores from pinned host slabs, overlapped")
+    h = headline_leg(torch, pool, layout, sources, dests, args.steps, args.warmup)
+    ms_per_step = 1000 * h["elapsed"] / args.steps
+    value = 2 * n * BF16_BLOCK_BYTES / (ms_per_step / 1000) / 1e9
+    link_gbs = h["link_bytes_per_step"] / (ms_per_step / 1000) / 1e9
+    log(f"step {ms_per_step:.3f} ms: {value:.1f} GB/s logical KV, {link_gbs:.2f} GB/s over the host link")
 
     k = kernel_leg(torch, ops, pool, sources, dests, scale_dtype, args.steps, args.warmup)
-    ms_per_step = 1000 * k["elapsed"] / args.steps
-    value = 2 * args.blocks * BF16_BLOCK_BYTES / (ms_per_step / 1000) / 1e9
     save_gbs = k["hbm_bytes"] / (k["save_ms"] / 1000) / 1e9
     restore_gbs = k["hbm_bytes"] / (k["restore_ms"] / 1000) / 1e9
     dominant = "save" if k["save_ms"] >= k["restore_ms"] else "restore"
@@ -918,7 +1305,8 @@ def main():
     kernel_name = (f"fp8_save_kernel<128, 2, 128, {scale_flag}, false>" if dominant == "save"
                    else f"fp8_restore_kernel<128, 2, 64, {scale_flag}, false>")
     traffic, traffic_source = pmc_traffic(kernel_name)
-    log(f"step {ms_per_step:.3f} ms; save {k['save_ms']:.3f} ms ({save_gbs:.0f} GB/s), "
+    hbm_step_ms = 1000 * k["elapsed"] / args.steps
+    log(f"entries in HBM: step {hbm_step_ms:.3f} ms; save {k['save_ms']:.3f} ms ({save_gbs:.0f} GB/s), "
         f"restore {k['restore_ms']:.3f} ms ({restore_gbs:.0f} GB/s)")
 
     result = {
@@ -935,25 +1323,39 @@ def main():
         "dtype": "f32",
         "data": "synthetic",
         "config": {
-            "workload": "qwen3-8b-kv-fp8-save-restore",
+            "workload": "qwen3-8b-kv-fp8-save-restore-pinned-host-slabs",
             "pool": list(shape),
-            "blocks_saved": args.blocks,
-            "blocks_restored": args.blocks,
+            "blocks_saved": n,
+            "blocks_restored": n,
             "scale_dtype": args.scale,
             "storage": "bf16 pool -> e4m3fn payload + per-(token, kv-head) scale",
+            "dtype_note": "the codec computes in fp32 (amax / 448, x / scale, code * scale); values are stored "
+                          "as bf16 in the pool and e4m3fn + scale in the entries",
             "values": "bf16 0.5*t(df=4), 4 outlier channels x20 per (kv, layer, head)",
-            "residency": "pool and entries in HBM",
+            "residency": "pool in HBM; saves write pinned host slabs (D2H), restores read pinned host slabs "
+                         "(H2D); the two directions overlap on the save and restore streams",
         },
-        "blocks_per_s": round(2 * args.blocks / (ms_per_step / 1000), 1),
+        "blocks_per_s": round(2 * n / (ms_per_step / 1000), 1),
+        "host_link": {
+            "bound": "pcie",
+            "achieved": round(link_gbs, 2),
+            "peak": 2 * PCIE_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(link_gbs / (2 * PCIE_PEAK_GBS), 4),
+            "bytes_per_step": h["link_bytes_per_step"],
+            "streams_concurrent": h["streams_concurrent"],
+        },
         "roofline": {
             "bound": "hbm",
-            "kernel": f"fp8_{dominant}_kernel",
+            "kernel": kernel_name,
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "traffic_source": traffic_source,
+            "workload": f"the same {n} + {n} blocks with entries in HBM, one launch each, HIP events on the "
+                        "launching stream",
         },
         "kernels": {
             "save": {"ms": round(k["save_ms"], 4), "hbm_gbs": round(save_gbs, 1),
@@ -961,7 +1363,10 @@ def main():
             "restore": {"ms": round(k["restore_ms"], 4), "hbm_gbs": round(restore_gbs, 1),
                         "frac": round(restore_gbs / HBM_PEAK_GBS, 4)},
             "algorithmic_bytes_per_launch": k["hbm_bytes"],
+            "hbm_resident_step": {"ms": round(hbm_step_ms, 4),
+                                  "logical_kv_gbs": round(2 * n * BF16_BLOCK_BYTES / (hbm_step_ms / 1000) / 1e9, 1)},
         },
+        "inventory": inventory,
     }
     if not args.skip_store:
         log("store_kvcache leg")
@@ -969,20 +1374,40 @@ def main():
     if args.calibrate_copy:
         raw_layout = ops.pool_layout(pool)
         _, _, raw_stride = ops.entry_layout(raw_layout, ops.FORMAT_RAW)
-        raw = torch.empty(args.blocks * raw_stride, dtype=torch.uint8, device=device)
-        ops.save_blocks(pool, sources, [raw.data_ptr() + i * raw_stride for i in range(args.blocks)],
-                        ops.FORMAT_RAW)
+        raw = torch.empty(n * raw_stride, dtype=torch.uint8, device=device)
+        ops.save_blocks(pool, sources, [raw.data_ptr() + i * raw_stride for i in range(n)], ops.FORMAT_RAW)
         torch.cuda.synchronize()
-        result["calibration_copy"] = {"kernel": "raw_copy_kernel", "read_bytes": args.blocks * BF16_BLOCK_BYTES,
-                                      "write_bytes": args.blocks * BF16_BLOCK_BYTES}
+        result["calibration_copy"] = {"kernel": "raw_copy_kernel", "read_bytes": n * BF16_BLOCK_BYTES,
+                                      "write_bytes": n * BF16_BLOCK_BYTES}
         del raw
     if not args.skip_host_link:
         log("host link leg")
-        result["host_link"] = host_link_leg(torch, pool, ops.pool_layout(pool, scale_dtype), sources, dests,
-                                            args.host_reps)
+        legs = host_link_leg(torch, pool, layout, sources, dests, args.host_reps)
+        link = result["host_link"]
+        link["legs"] = legs
+        ceiling = legs.get("ceiling_memcpy_duplex_gbs")
+        if ceiling:
+            link["measured_ceiling"] = ceiling
+            link["frac_of_measured_ceiling"] = round(link_gbs / ceiling, 4)
+        if not args.skip_sdma_probe:
+            log("host link: explicit SDMA engines")
+            link["sdma_probe"] = sdma_probe(torch, legs["bytes_per_direction"])
+            log("host link: copies beside HBM-bound kernels")
+            hbm_entries = torch.empty(n * k["entry_stride"], dtype=torch.uint8, device=device)
+            entries = [hbm_entries.data_ptr() + i * k["entry_stride"] for i in range(n)]
+            ops.save_blocks(pool, sources, entries, ops.FORMAT_FP8, scale_dtype)
+            link["interference"] = interference_leg(torch, kvx_kernels={
+                f"kvx FP8 restore of {n} blocks (entries in HBM)":
+                    lambda: ops.restore_blocks(pool, dests, entries, ops.FORMAT_FP8, scale_dtype),
+                f"kvx FP8 save of {n} blocks (entries in HBM)":
+                    lambda: ops.save_blocks(pool, sources, entries, ops.FORMAT_FP8, scale_dtype)})
+            del hbm_entries
+            log(f"interference: {json.dumps(link['interference'])}")
+        log(f"host link legs: D2H {legs['save_d2h_gbs']}, H2D {legs['restore_h2d_gbs']}, duplex {legs['duplex_gbs']} "
+            f"GB/s (memcpy ceiling {ceiling}); SDMA probe {json.dumps(link.get('sdma_probe'))}")
     if not args.skip_reference_gpu:
         log("reference torch codec on the GPU")
-        result["reference_torch_gpu"] = reference_gpu_leg(torch, pool, sources, dests, scale_dtype, ms_per_step)
+        result["reference_torch_gpu"] = reference_gpu_leg(torch, pool, sources, dests, scale_dtype, hbm_step_ms)
         if not args.skip_host_link:
             log("reference host path on the GPU")
             result["reference_torch_gpu"]["host_link"] = reference_link_leg(torch, pool, sources, dests, scale_dtype)
@@ -1005,7 +1430,7 @@ def main():
         result["agent_pressure"] = agent_leg(torch, pool, scale_dtype)
     if not args.skip_cpu_baseline:
         log("cpu baseline leg")
-        result["cpu_baseline"] = cpu_baseline_leg(torch, shape, scale_dtype, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline_leg(torch, pool, sources, dests, scale_dtype, inventory)
     print(json.dumps(result), flush=True)
 
 

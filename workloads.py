@@ -6,6 +6,7 @@ Values are generated on the pool's device, one (K/V, layer) plane at a time,
 with a torch.Generator seeded per plane so any plane can be regenerated.
 """
 
+import time
 from dataclasses import dataclass
 
 import numpy as np
@@ -128,8 +129,11 @@ class SyntheticKVRunner:
     nanovllm's ModelRunner does (model_runner.py:156-166, 186) and uploads
     it, the token ids and the positions through pinned memory without
     blocking the host (:169-173, 187-190), writes synthetic_kv rows for all
-    layers through kvx.ops.store_kvcache on the current stream and returns
-    `next_token` for each sequence.
+    layers through kvx.ops.store_kvcache on the current stream, then
+    "samples" `next_token` for each sequence on the device and reads the
+    tokens back, which blocks the host until the step's GPU work is done, as
+    the reference's sampler readback does (:223). `blocked_s` adds up the
+    host time spent in those readbacks.
     """
 
     def __init__(self, pool: torch.Tensor, next_token: int = 1):
@@ -138,6 +142,7 @@ class SyntheticKVRunner:
         self.block_size = pool.shape[3]
         self.next_token = next_token
         self.tokens_written = 0
+        self.blocked_s = 0.0
 
     def call(self, method, *args):
         if method == "exit":
@@ -169,7 +174,11 @@ class SyntheticKVRunner:
             for layer in range(pool.shape[1]):
                 ops.store_kvcache(kv[0, layer], kv[1, layer], pool[0, layer], pool[1, layer], mapping)
             self.tokens_written += len(slots)
-        return [self.next_token] * len(seqs)
+        sampled = torch.full((len(seqs),), self.next_token, dtype=torch.int64, device=self.kv_cache.device)
+        t0 = time.perf_counter()
+        tokens = sampled.tolist()
+        self.blocked_s += time.perf_counter() - t0
+        return tokens
 
 
 def expected_block(pool: torch.Tensor, token_ids, start_position: int) -> torch.Tensor:
@@ -192,6 +201,8 @@ class AgentPressureResult:
     h2d_bytes: int
     blocks_checked: int
     blocks_fp8_round_trip: int
+    host_blocked_s: float = 0.0  # in the runner's token readbacks
+    drain_s: float = 0.0         # after the last step, waiting for the copy streams and the GPU
 
     @property
     def link_gbs(self) -> float:
@@ -213,8 +224,6 @@ def run_agent_pressure(engine, agents: int = 4, context: int = 32768, turns: int
     the current agent's own cached blocks (the least recently used ones), which its admission would then
     restore again.
     """
-    import time
-
     from kvx import ops
     from kvx.engine.sequence import SamplingParams, Sequence
 
@@ -225,6 +234,7 @@ def run_agent_pressure(engine, agents: int = 4, context: int = 32768, turns: int
     bs = pool.shape[3]
     params = SamplingParams(temperature=0, max_tokens=1, ignore_eos=True)
     checked = fp8_hits = 0
+    blocked_before = getattr(engine.model_runner, "blocked_s", 0.0)
     t0 = time.perf_counter()
     for turn in range(turns):
         for a in range(agents):
@@ -271,12 +281,16 @@ def run_agent_pressure(engine, agents: int = 4, context: int = 32768, turns: int
             if nxt is not None:
                 # The request finished in one step: hint once it is checked (the prefetch may recycle its blocks).
                 engine.prefetch_prefix(nxt)
+    t_drain = time.perf_counter()
     if cache is not None:
         cache.synchronize()
     torch.cuda.synchronize(pool.device)
     wall = time.perf_counter() - t0
+    drain = time.perf_counter() - t_drain
     stats = cache.stats if cache is not None else {"saved_blocks": 0, "restored_blocks": 0, "budget_skips": 0}
     entry = cache.block_bytes if cache is not None else 0
+    blocked = getattr(engine.model_runner, "blocked_s", 0.0) - blocked_before
     return AgentPressureResult(turns * agents, wall, stats["saved_blocks"], stats["restored_blocks"],
                                cache.prefetched_blocks if cache is not None else 0, stats["budget_skips"],
-                               stats["saved_blocks"] * entry, stats["restored_blocks"] * entry, checked, fp8_hits)
+                               stats["saved_blocks"] * entry, stats["restored_blocks"] * entry, checked, fp8_hits,
+                               blocked, drain)
