@@ -1,7 +1,7 @@
 """kvx: MI355X-native KV-block copy path (libkvx HIP kernels behind a C ABI).
 
 Drop-ins for the reference package's copy path:
-  kvx.layers.attention.store_kvcache        <- nanovllm.layers.attention.store_kvcache
+  kvx.ops.store_kvcache                     <- nanovllm.layers.attention.store_kvcache
   kvx.engine.cpu_prefix_cache.CPUBlockCache <- nanovllm.engine.cpu_prefix_cache.CPUBlockCache
   kvx.engine.kv_handoff                     <- nanovllm.engine.kv_handoff (plus an FP8 payload)
   kvx.ops                                   the operator API (codec, block lists, token copies, test hooks)
