@@ -128,9 +128,10 @@ def kernel_leg(torch, ops, pool, sources, dests, scale_dtype, steps, warmup):
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for ev in events:
-        step(ev)
-    torch.cuda.synchronize()
+    with marked("kernel leg: timed steps"):
+        for ev in events:
+            step(ev)
+        torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     save_ms = sum(e[0].elapsed_time(e[1]) for e in events) / steps
     restore_ms = sum(e[1].elapsed_time(e[2]) for e in events) / steps
@@ -148,6 +149,10 @@ def store_leg(torch, ops, pool, reps=5, concurrency=True):
     padded to a multiple of 256 with -1 slots. `paged_blocks` times the same
     batch with the slot layout a model runner produces (model_runner.py:156-166):
     each sequence gets seeded random distinct blocks and fills them in order.
+    `contiguous_slots` writes the batch to consecutive slots (streaming
+    destinations). `writes_only` prices each slot pattern alone: the same
+    kernel with K and V expanded from one row (row stride 0), so every token's
+    source is one cached 4 KiB row and HBM sees only the destination rows.
     """
     import numpy as np
 
@@ -165,12 +170,12 @@ def store_leg(torch, ops, pool, reps=5, concurrency=True):
     stream = torch.cuda.current_stream(pool.device)
     row = heads * hd * 2
 
-    def timed(slot_map, tokens):
+    def timed(slot_map, tokens, sources=(key, value)):
         mapping = torch.from_numpy(slot_map).to(pool.device)
 
         def run():
             for layer in range(layers):
-                ops.store_kvcache(key, value, pool[0, layer], pool[1, layer], mapping)
+                ops.store_kvcache(*sources, pool[0, layer], pool[1, layer], mapping)
 
         run()
         times = []
@@ -217,6 +222,15 @@ def store_leg(torch, ops, pool, reps=5, concurrency=True):
     out["contiguous_slots"] = {"tokens": total, "ms_all_layers": round(1000 * t, 4), "hbm_gbs": round(gbs, 1),
                                "frac": round(gbs / HBM_PEAK_GBS, 4)}
     out["random_vs_contiguous"] = round(out["hbm_gbs"] / gbs, 4)
+    one_row = (key[:1].expand(padded, heads, hd), value[:1].expand(padded, heads, hd))
+    written = {}
+    for name, slot_map, tokens in (("random", slots, total), ("paged_blocks", paged, pos),
+                                   ("contiguous", contiguous, total)):
+        t, _, _ = timed(slot_map, tokens, one_row)
+        wgbs = layers * (tokens * 2 * row + padded * 4) / t / 1e9
+        written[name] = {"ms_all_layers": round(1000 * t, 4), "write_gbs": round(wgbs, 1),
+                         "frac": round(wgbs / HBM_PEAK_GBS, 4)}
+    out["writes_only"] = written
     if concurrency:
         out["with_concurrent_saves"] = store_beside_saves(torch, ops, pool, key, value, lengths, reps)
     return out
