@@ -198,3 +198,30 @@ def test_store_kvcache_closed_form_matches_a_loop():
             k_loop.reshape(slots, -1)[s] = key[i].ravel()
             v_loop.reshape(slots, -1)[s] = value[i].ravel()
     assert np.array_equal(k, k_loop) and np.array_equal(v, v_loop)
+
+
+@pytest.mark.parametrize("count", [1, 4, 5, 11, 12])
+def test_token_gather_matches_a_per_token_loop(count):
+    """Token t of a handoff payload is row t % BS of block table[t // BS] (kv_handoff.py:51-55)."""
+    rng = np.random.default_rng(count)
+    pool = rng.integers(0, 1 << 16, size=(2, 3, 5, 4, 2, 3), dtype=np.uint16)
+    table = [3, 0, 4]
+    dense = oracle.gather_tokens(pool, table, count)
+    assert dense.shape == (2, 3, count, 2, 3)
+    for t in range(count):
+        assert np.array_equal(dense[:, :, t], pool[:, :, table[t // 4], t % 4]), f"token {t}"
+
+
+@pytest.mark.parametrize("count", [1, 4, 6, 12])
+def test_token_scatter_writes_exactly_the_payload_rows(count):
+    """Scatter puts token t at row t % BS of block table[t // BS] (kv_handoff.py:112-118) and touches nothing else."""
+    rng = np.random.default_rng(100 + count)
+    pool = rng.integers(0, 1 << 16, size=(2, 3, 5, 4, 2, 3), dtype=np.uint16)
+    dense = rng.integers(0, 1 << 16, size=(2, 3, count, 2, 3), dtype=np.uint16)
+    table = [2, 4, 1]
+    want = pool.copy()
+    for t in range(count):
+        want[:, :, table[t // 4], t % 4] = dense[:, :, t]
+    oracle.scatter_tokens(pool, table, dense)
+    assert np.array_equal(pool, want)
+    assert np.array_equal(oracle.gather_tokens(pool, table, count), dense)
