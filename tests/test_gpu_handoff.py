@@ -162,19 +162,22 @@ def test_detach_then_resume_carries_the_kv_and_decode_continues(gpu, length, fmt
 
 @pytest.mark.parametrize("fmt", FORMATS)
 def test_import_leaves_the_payload_free_for_reuse(gpu, fmt):
-    """Once resume_request returns, the snapshot's pinned memory may be dropped and reused at once."""
+    """Once import_kv returns, the snapshot's pinned memory may be dropped and reused at once.
+
+    import_kv is called directly, not through resume_request, so nothing
+    but import_kv itself orders the payload's last read before the reuse.
+    """
     source, source_id = running_request(gpu, length=700, budget=1024)
     snapshot = source.detach_request(source_id, **fmt)
     expected = kv_handoff.KVSnapshot(**{**snapshot.__dict__, "kv": snapshot.kv.clone(),
                                         "scale": None if snapshot.scale is None else snapshot.scale.clone()})
     destination = cached_engine(gpu, [[11]])
-    destination.resume_request(snapshot)
+    seq = kv_handoff.import_kv(destination.model_runner, destination.scheduler.block_manager, snapshot)
     nbytes = snapshot.payload_bytes
     del snapshot
     for _ in range(4):  # the host allocator hands the freed pinned blocks out again
         junk = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
         junk.fill_(0x5A)
-    seq = destination.scheduler.running[0]
     assert kv_handoff.verify_imported_kv(destination.model_runner, seq, expected)
 
 
