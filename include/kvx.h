@@ -176,7 +176,8 @@ typedef struct kvx_cache kvx_cache;
 /* Creates an engine for `pool` on `device` using the caller's two streams (non-NULL). */
 int kvx_cache_create(void* pool, const kvx_block_layout* layout, int32_t format, void* save_stream,
                      void* restore_stream, int32_t device, kvx_cache** out);
-/* Synchronises both streams, then frees the engine's events (:431-448). */
+/* Synchronises both streams and the restores queued on callers' streams, then frees the engine's events
+ * (:431-448). */
 int kvx_cache_destroy(kvx_cache* cache);
 /*
  * Attaches one device staging area per stream, each holding `entries`
@@ -249,7 +250,8 @@ int kvx_cache_restore(kvx_cache* cache, const int32_t* slots_host, const int32_t
 int kvx_cache_before_block_reuse(kvx_cache* cache, int32_t block_id, void* compute_stream);
 /* Orders later reads of block_id on compute_stream after its pending restore (:359-363). */
 int kvx_cache_before_block_use(kvx_cache* cache, int32_t block_id, void* compute_stream);
-/* Blocks the host until both streams are idle (synchronize, :270-273). */
+/* Blocks the host until both streams are idle and every restore queued on a caller's stream has completed
+ * (synchronize, :270-273). */
 int kvx_cache_synchronize(kvx_cache* cache);
 /* Counts of engine activity: saves, restores, waits inserted; for tests and stats. */
 int kvx_cache_counters(kvx_cache* cache, int64_t* saved_blocks, int64_t* restored_blocks,

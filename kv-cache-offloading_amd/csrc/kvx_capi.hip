@@ -344,6 +344,11 @@ struct kvx_cache {
   std::vector<Event*> slot_read, slot_saved;          // per host slot
   std::vector<Event*> free_events, all_events;
   Event* last_save = nullptr;  // the latest save's completion
+  // Completions of restores queued on callers' streams (waited direct
+  // restores) not yet seen complete. synchronize and destroy wait for them as
+  // for the engine's own streams: such a restore still reads its host slot,
+  // and the slot's memory may be released once those calls return.
+  std::vector<Event*> caller_reads;
   bool host_reads_ok = false;  // restores may read host slots with the striding kernel
   int64_t saved = 0, restored = 0, waits = 0;
   int32_t debug = 0;  // KVX_DEBUG_* negative-control flags
@@ -399,6 +404,31 @@ struct kvx_cache {
 
   void release_if_unused(Event* e) {
     if (e->refs == 0) free_events.push_back(e);
+  }
+
+  // Keeps `e` (recorded on a caller's stream) until it is seen complete;
+  // drops the tracked events that already are.
+  void track_caller_read(Event* e) {
+    size_t kept = 0;
+    for (Event* t : caller_reads) {
+      if (hipEventQuery(t->ev) == hipSuccess) unref(t);
+      else caller_reads[kept++] = t;
+    }
+    caller_reads.resize(kept);
+    ++e->refs;
+    caller_reads.push_back(e);
+  }
+
+  // Blocks until every tracked caller-stream restore has completed.
+  int sync_caller_reads() {
+    int rc = KVX_OK;
+    for (Event*& t : caller_reads) {
+      const int r = hip_status(hipEventSynchronize(t->ev), "hipEventSynchronize");
+      if (!rc) rc = r;
+      unref(t);
+    }
+    caller_reads.clear();
+    return rc;
   }
 
   // `s` waits for `e`. An event that has already completed orders nothing
@@ -484,7 +514,8 @@ struct kvx_cache {
   // Restores of one or two blocks whose caller waits for them (wait != 0),
   // issued while no save is in flight, have the restore kernel read the host
   // slots itself: a capped grid strides over the tiles with system-scope
-  // loads. Everything else goes through device staging and an H2D copy.
+  // loads, queued on the caller's stream (kvx_cache_restore). Everything else
+  // goes through device staging and an H2D copy on the restore stream.
   // Measured on MI355X with one engine call per block (the reference
   // BlockManager's pattern): waited restores 47.8 -> 48.3 GB/s (FP8) and
   // 51.1 -> 54.1 (BF16); the agent-pressure workload 3.34 -> 3.09 s. Not for
@@ -758,6 +789,8 @@ int kvx_cache_destroy(kvx_cache* c) {
     int rc2 = hip_status(hipStreamSynchronize(c->restore_stream), "hipStreamSynchronize");
     if (!rc) rc = rc2;
   }
+  const int rc3 = c->sync_caller_reads();
+  if (!rc) rc = rc3;
   for (Event* e : c->all_events) {
     (void)hipEventDestroy(e->ev);
     delete e;
@@ -888,6 +921,7 @@ int kvx_cache_restore(kvx_cache* c, const int32_t* slots, const int32_t* ids, in
   Event* done = nullptr;
   rc = c->new_event(&done);
   if (!rc) rc = hip_status(hipEventRecord(done->ev, s), "hipEventRecord");
+  if (!rc && s == compute) c->track_caller_read(done);
   if (!rc && wait && s != compute) rc = c->queue_wait(compute, done);
   if (rc) {
     if (done) c->release_if_unused(done);
@@ -949,6 +983,7 @@ int kvx_cache_synchronize(kvx_cache* c) {
   int rc = scope.enter(c->device);
   if (!rc) rc = hip_status(hipStreamSynchronize(c->save_stream), "hipStreamSynchronize");
   if (!rc && c->split) rc = hip_status(hipStreamSynchronize(c->restore_stream), "hipStreamSynchronize");
+  if (!rc) rc = c->sync_caller_reads();
   return rc;
 }
 

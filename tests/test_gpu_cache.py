@@ -512,6 +512,37 @@ def test_engine_restores_of_every_path_write_the_oracle_bytes(gpu, fmt, scale_dt
         engine.close()
 
 
+@pytest.mark.parametrize("ending", ["synchronize", "close"])
+def test_waited_restores_on_the_callers_stream_finish_before_synchronize_and_close_return(gpu, ending):
+    # A waited one-block restore with no save in flight reads its host slot from the caller's stream. Queued
+    # behind a delay there, it is still pending when synchronize() or close() is called; once either returns,
+    # the slot's pinned memory may be overwritten (or released and reused) without touching the restore.
+    from kvx.engine.cpu_prefix_cache import _CopyEngine
+
+    g = torch.Generator(device=gpu).manual_seed(21)
+    pool = torch.randn((2, 4, 4, BS, 8, 128), generator=g, device=gpu).to(torch.bfloat16)
+    layout = ops.pool_layout(pool, torch.float32)
+    engine = _CopyEngine(pool, layout, ops.FORMAT_FP8, split=True)
+    stride = engine.entry_stride
+    slab = torch.empty(2 * stride, dtype=torch.uint8, pin_memory=True)
+    staging = [torch.empty(2 * stride, dtype=torch.uint8, device=gpu) for _ in range(2)]
+    engine.add_slab(slab, 2)
+    engine.set_staging(*staging, 2)
+    caller = torch.cuda.current_stream(gpu)
+    try:
+        engine.save([1], [0], caller.cuda_stream)
+        engine.synchronize()
+        codes, scales = oracle.save_block_fp8(bf16_bits(pool), 1, True)
+        ops.sleep(DELAY_US, stream=caller, device=gpu)
+        engine.restore([0], [3], True, caller.cuda_stream)
+        getattr(engine, ending)()
+        slab.fill_(0x7F)  # e4m3 NaN codes: a restore still reading the slot would land them
+        torch.cuda.synchronize()
+        assert np.array_equal(bf16_bits(pool[:, :, 3]), oracle.dequantize(codes, scales, True))
+    finally:
+        engine.close()
+
+
 def test_a_failed_batch_withdraws_the_metadata_it_published(gpu, monkeypatch):
     pool = make_pool(gpu, 6)
     manager = BlockManager(6, BS)
