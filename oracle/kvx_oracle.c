@@ -1,7 +1,7 @@
 /*
  * kvx_oracle.c — CPU restatement of the reference's FP8 KV codec.
  *
- * TEST INFRASTRUCTURE ONLY. This file is the checker the tests, smoke() and
+ * TEST INFRASTRUCTURE ONLY. This file is the oracle the tests, smoke() and
  * bench.py's CPU baseline compare libkvx against; no product code links or
  * loads it.
  *

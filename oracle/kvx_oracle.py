@@ -1,7 +1,7 @@
 """Python face of the oracle: the C restatement (kvx_oracle.c) plus numpy closed forms.
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
-bench.py's CPU baseline as the checker. Product code never imports it.
+bench.py's CPU baseline, to check libkvx against. Product code never imports it.
 
 Everything here works on bit patterns held in numpy integer arrays (bf16 as
 uint16, fp8 as uint8, fp32 scales as float32), so comparisons are bit-exact.
