@@ -344,11 +344,13 @@ struct kvx_cache {
   std::vector<Event*> slot_read, slot_saved;          // per host slot
   std::vector<Event*> free_events, all_events;
   Event* last_save = nullptr;  // the latest save's completion
-  // Completions of restores queued on callers' streams (waited direct
-  // restores) not yet seen complete. synchronize and destroy wait for them as
-  // for the engine's own streams: such a restore still reads its host slot,
-  // and the slot's memory may be released once those calls return.
-  std::vector<Event*> caller_reads;
+  // Per caller stream, the completion of the latest restore queued on it
+  // (waited direct restores), until seen complete. Work on one stream
+  // completes in order, so the latest covers the earlier ones. synchronize
+  // and destroy wait for them as for the engine's own streams: such a
+  // restore still reads its host slot, and the slot's memory may be released
+  // once those calls return.
+  std::vector<std::pair<hipStream_t, Event*>> caller_reads;
   bool host_reads_ok = false;  // restores may read host slots with the striding kernel
   int64_t saved = 0, restored = 0, waits = 0;
   int32_t debug = 0;  // KVX_DEBUG_* negative-control flags
@@ -406,23 +408,31 @@ struct kvx_cache {
     if (e->refs == 0) free_events.push_back(e);
   }
 
-  // Keeps `e` (recorded on a caller's stream) until it is seen complete;
-  // drops the tracked events that already are.
-  void track_caller_read(Event* e) {
+  // Tracks `e`, just recorded on caller stream `s`, in place of the stream's
+  // previous one; drops other streams' events that have completed.
+  void track_caller_read(hipStream_t s, Event* e) {
+    ++e->refs;
     size_t kept = 0;
-    for (Event* t : caller_reads) {
-      if (hipEventQuery(t->ev) == hipSuccess) unref(t);
-      else caller_reads[kept++] = t;
+    bool placed = false;
+    for (auto& [stream, t] : caller_reads) {
+      if (stream == s) {
+        unref(t);
+        t = e;
+        placed = true;
+      } else if (hipEventQuery(t->ev) == hipSuccess) {
+        unref(t);
+        continue;
+      }
+      caller_reads[kept++] = {stream, t};
     }
     caller_reads.resize(kept);
-    ++e->refs;
-    caller_reads.push_back(e);
+    if (!placed) caller_reads.emplace_back(s, e);
   }
 
   // Blocks until every tracked caller-stream restore has completed.
   int sync_caller_reads() {
     int rc = KVX_OK;
-    for (Event*& t : caller_reads) {
+    for (auto& [stream, t] : caller_reads) {
       const int r = hip_status(hipEventSynchronize(t->ev), "hipEventSynchronize");
       if (!rc) rc = r;
       unref(t);
@@ -921,7 +931,7 @@ int kvx_cache_restore(kvx_cache* c, const int32_t* slots, const int32_t* ids, in
   Event* done = nullptr;
   rc = c->new_event(&done);
   if (!rc) rc = hip_status(hipEventRecord(done->ev, s), "hipEventRecord");
-  if (!rc && s == compute) c->track_caller_read(done);
+  if (!rc && s == compute) c->track_caller_read(s, done);
   if (!rc && wait && s != compute) rc = c->queue_wait(compute, done);
   if (rc) {
     if (done) c->release_if_unused(done);
