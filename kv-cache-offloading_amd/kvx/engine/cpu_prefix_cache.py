@@ -17,6 +17,7 @@ torch-op path for CPU-resident pools.
 """
 
 import ctypes
+from collections import Counter
 from contextlib import contextmanager
 from dataclasses import dataclass
 from math import prod
@@ -50,7 +51,7 @@ class _CPUBlock:
 
 
 class CPUCacheFullError(MemoryError):
-    """The configured payload budget cannot admit another block."""
+    """save_block found the byte budget spent: no further entry fits."""
 
 
 # Copy streams must run side by side with each other and with the compute
@@ -268,77 +269,165 @@ class _CopyBatcher:
             raise
 
 
-class CPUBlockCache:
-    """One engine's bounded payload store, with optional automatic integration.
+def _checked_costs(costs) -> tuple[float, float, float]:
+    """Hybrid admission costs (restore s/block, recompute s/token, recompute s/token^2), each >= 0."""
+    if len(costs) != 3 or min(costs) < 0:
+        raise ValueError("hybrid needs three nonnegative cost coefficients")
+    return tuple(float(c) for c in costs)
 
-    Keys are the engine's chained prefix hashes, not physical block IDs. The
-    byte budget covers tensor payloads (plus FP8 scales), not Python
-    metadata. Restored GPU entries are recyclable, not pinned; the CPU copy
-    survives until discard/clear/close. Behaviour of every option follows
-    cpu_prefix_cache.py:44-70: save_on_release saves a published block when
-    its last owner releases it while admission is blocked; prefetch restores
-    a blocked request's CPU hits into spare blocks in the background; fp8
-    stores float8_e4m3fn payloads with one scale per (token, KV head) row in
-    `scale_dtype` (default: the pool dtype, as the reference); hybrid =
-    (restore_s_per_block, recompute_s_per_token, recompute_s_per_token2)
-    lets admission recompute a CPU-only prefix's head while its tail restores.
-    Call synchronize() before reading payloads on the host.
+
+def _checked_pool(runner, manager: BlockManager, max_bytes, automatic: bool, save_on_release: bool,
+                  prefetch: bool, hybrid, fp8: bool, scale_dtype) -> torch.Tensor:
+    """The runner's KV pool, once the cache's arguments fit it and this library (cpu_prefix_cache.py:76-91).
+
+    Raises, in this order: a bad budget, tensor parallelism, automatic-only
+    options without automatic=True, bad hybrid costs, a pool that does not
+    match the block manager, and what libkvx cannot copy (a pool off the
+    GPU, non-contiguous, or FP8 from a non-bf16 pool or with an unsupported
+    scale dtype).
+    """
+    if type(max_bytes) is not int or max_bytes <= 0:
+        raise ValueError("max_bytes must be a positive integer")
+    if runner.world_size != 1:
+        raise NotImplementedError("CPU prefix blocks currently require TP=1")
+    if (save_on_release or prefetch or hybrid) and not automatic:
+        raise ValueError("save_on_release, prefetch and hybrid require automatic=True")
+    if hybrid is not None:
+        _checked_costs(hybrid)
+    pool = runner.kv_cache
+    geometry_ok = (pool.ndim == 6 and pool.shape[0] == 2 and min(pool.shape) > 0
+                   and pool.shape[2] == len(manager.blocks)
+                   and pool.shape[3] == manager.block_size == runner.block_size)
+    if not geometry_ok:
+        raise ValueError("KV pool layout does not match the block manager")
+    if pool.device.type != "cuda":
+        raise ValueError("KV pool must be on a ROCm device (libkvx copies blocks with HIP kernels)")
+    if not pool.is_contiguous():
+        raise ValueError("KV pool must be contiguous")
+    if fp8 and (pool.dtype != torch.bfloat16 or scale_dtype not in ops.SCALE_DTYPES):
+        raise NotImplementedError("FP8 payloads need a bfloat16 pool and a bfloat16/float32 scale")
+    return pool
+
+
+class _HostSlots:
+    """A cache's pinned host entries, registered with its copy engine.
+
+    Slots are allocated a chunk at a time, ~1 GiB per page-locking call
+    (never beyond `capacity`), and one chunk holds its entries back to back,
+    `entry_stride` apart: the payload, then the scales at `scale_offset`, so
+    one DMA moves a block. Free slots form a stack: a fresh chunk hands out
+    its lowest slot first and a returned slot is the next one taken
+    (cpu_prefix_cache.py:199-208). Typed views with the reference's slab
+    shapes ([count, 2, L, BS, H, hd] payloads, [..., 1] scales) are kept per
+    chunk.
+    """
+
+    def __init__(self, engine: _CopyEngine, capacity: int, entry_bytes: int, kv_shape, kv_dtype,
+                 scale_shape, scale_dtype):
+        self.engine = engine
+        self.capacity = capacity
+        self.entry_bytes = entry_bytes  # the budget's unit: payload plus scales
+        self.kv_shape, self.kv_dtype = kv_shape, kv_dtype
+        self.scale_shape, self.scale_dtype = scale_shape, scale_dtype
+        self.memory: list[torch.Tensor] = []
+        self.kv_views: list[torch.Tensor] = []
+        self.scale_views: list[torch.Tensor] = []
+        self.free: list[int] = []
+        self.count = 0
+
+    def _add_chunk(self):
+        n = min(max(1, _SLAB_CHUNK_BYTES // self.entry_bytes), self.capacity - self.count)
+        stride = self.engine.entry_stride
+        memory = torch.empty(n * stride, dtype=torch.uint8, device="cpu", pin_memory=True)
+        entries = memory.view(n, stride)
+        kv_bytes = prod(self.kv_shape) * self.kv_dtype.itemsize
+        self.kv_views.append(entries[:, :kv_bytes].view(self.kv_dtype).view(n, *self.kv_shape))
+        if self.scale_shape is not None:
+            at = self.engine.scale_offset
+            nbytes = prod(self.scale_shape) * self.scale_dtype.itemsize
+            self.scale_views.append(entries[:, at:at + nbytes].view(self.scale_dtype).view(n, *self.scale_shape))
+        self.engine.add_slab(memory, n)
+        self.memory.append(memory)
+        self.free.extend(reversed(range(self.count, self.count + n)))
+        self.count += n
+
+    def take(self) -> int:
+        if not self.free:
+            self._add_chunk()
+        return self.free.pop()
+
+    def give_back(self, slot: int):
+        self.free.append(slot)
+
+    def reserve_all(self):
+        while self.count < self.capacity:
+            self._add_chunk()
+
+    def view(self, slot: int) -> tuple[torch.Tensor, torch.Tensor | None]:
+        """(payload, scale or None) of one slot, as views of its pinned entry."""
+        base = 0
+        for i, kv in enumerate(self.kv_views):
+            if slot < base + len(kv):
+                scale = self.scale_views[i][slot - base] if self.scale_views else None
+                return kv[slot - base], scale
+            base += len(kv)
+        raise IndexError(slot)
+
+    def release(self):
+        for items in (self.memory, self.kv_views, self.scale_views, self.free):
+            items.clear()
+        self.count = 0
+
+
+class CPUBlockCache:
+    """A bounded store of KV blocks in pinned host memory, keyed by the engine's chained prefix hashes.
+
+    The drop-in for cpu_prefix_cache.py:44-448: the same constructor
+    options, properties, hooks, budget and errors. The budget counts entry
+    bytes (FP8 payload plus scales, or the bf16 block), not Python metadata.
+    A restored block is an ordinary idle GPU hit that can be recycled; its
+    CPU entry stays until discard, clear or close.
+
+    Options (each as the reference's): automatic attaches the cache to the
+    block manager, which then saves published blocks it recycles and
+    restores CPU hits on admission; save_on_release also saves a published
+    block when its last owner releases it while an admission is blocked;
+    prefetch lets the scheduler restore a blocked request's CPU hits into
+    spare blocks in the background; split_streams gives restores their own
+    stream, so saves and restores share the host link in both directions;
+    fp8 stores float8_e4m3fn payloads with one scale per (token, KV head)
+    row in `scale_dtype` (default: the pool dtype, as the reference); hybrid
+    = (restore s/block, recompute s/token, recompute s/token^2) lets an
+    admission recompute the head of a CPU-only prefix while its tail
+    restores; preallocate pins the whole budget up front.
+
+    Copies run in libkvx (see _CopyEngine and _CopyBatcher); call
+    synchronize() before reading payloads on the host.
     """
 
     def __init__(self, runner, block_manager: BlockManager, max_bytes: int, *,
                  automatic: bool = False, save_on_release: bool = False, preallocate: bool = False,
                  prefetch: bool = False, split_streams: bool = False, fp8: bool = False,
                  hybrid: tuple[float, float, float] | None = None, scale_dtype: torch.dtype | None = None):
-        if type(max_bytes) is not int or max_bytes <= 0:
-            raise ValueError("max_bytes must be a positive integer")
-        if runner.world_size != 1:
-            raise NotImplementedError("CPU prefix blocks currently require TP=1")
-        if (save_on_release or prefetch or hybrid) and not automatic:
-            raise ValueError("save_on_release, prefetch and hybrid require automatic=True")
-        if hybrid is not None and (len(hybrid) != 3 or min(hybrid) < 0):
-            raise ValueError("hybrid needs three nonnegative cost coefficients")
-        cache = runner.kv_cache
-        if (cache.ndim != 6 or cache.shape[0] != 2 or min(cache.shape) <= 0
-                or cache.shape[2] != len(block_manager.blocks)
-                or cache.shape[3] != block_manager.block_size
-                or runner.block_size != block_manager.block_size):
-            raise ValueError("KV pool layout does not match the block manager")
-        if cache.device.type != "cuda":
-            raise ValueError("KV pool must be on a ROCm device (libkvx copies blocks with HIP kernels)")
-        if not cache.is_contiguous():
-            raise ValueError("KV pool must be contiguous")
-        scale_dtype = cache.dtype if scale_dtype is None else scale_dtype
-        if fp8 and (cache.dtype != torch.bfloat16 or scale_dtype not in ops.SCALE_DTYPES):
-            raise NotImplementedError("FP8 payloads need a bfloat16 pool and a bfloat16/float32 scale")
-        self._cache = cache
-        self._manager = block_manager
-        self._shape = (2, cache.shape[1], *cache.shape[3:])
-        self._fp8 = fp8
-        self._dtype = torch.float8_e4m3fn if fp8 else cache.dtype
-        self._scale_dtype = scale_dtype
-        self._scale_shape = (*self._shape[:-1], 1)
-        self._block_bytes = prod(self._shape) * self._dtype.itemsize
-        if fp8:
-            self._block_bytes += prod(self._scale_shape) * scale_dtype.itemsize
+        pool = runner.kv_cache
+        scale_dtype = pool.dtype if scale_dtype is None else scale_dtype
+        pool = _checked_pool(runner, block_manager, max_bytes, automatic, save_on_release, prefetch, hybrid, fp8,
+                             scale_dtype)
+        self._hybrid = None if hybrid is None else _checked_costs(hybrid)
+        self._fp8, self._scale_dtype = fp8, scale_dtype
+        self._save_on_release, self._prefetch = save_on_release, prefetch
+        self._cache, self._manager = pool, block_manager
+        self._shape = (2, pool.shape[1], *pool.shape[3:])  # one block: [K/V, layer, token, KV head, head dim]
         self._max_bytes = max_bytes
+        self._layout = ops.pool_layout(pool, scale_dtype if fp8 else None)
+        self._engine = _CopyEngine(pool, self._layout, ops.FORMAT_FP8 if fp8 else ops.FORMAT_RAW, split_streams)
+        entry_bytes = self._engine.logical_bytes  # kvx_entry_layout: payload plus scales, as the reference counts
+        self._slots = _HostSlots(self._engine, max_bytes // entry_bytes, entry_bytes, self._shape,
+                                 torch.float8_e4m3fn if fp8 else pool.dtype,
+                                 (*self._shape[:-1], 1) if fp8 else None, scale_dtype)
         self._entries: dict[int, _CPUBlock] = {}
-        self._capacity = max_bytes // self._block_bytes
-        self._slabs: list[torch.Tensor] = []  # payload views [count, 2, L, BS, H, hd]
-        self._scale_slabs: list[torch.Tensor] = []  # FP8 scale views [count, 2, L, BS, H, 1]
-        self._slab_memory: list[torch.Tensor] = []  # the pinned allocations
-        self._free_slots: list[int] = []
-        self._num_slots = 0
-        self._hybrid = hybrid
-        self._save_on_release = save_on_release
-        self._prefetch = prefetch
-        self._prefetched_blocks = 0
-        self._saved_blocks = 0
-        self._restored_blocks = 0
-        self._budget_skips = 0
-        self._layout = ops.pool_layout(cache, scale_dtype if fp8 else None)
-        fmt = ops.FORMAT_FP8 if fp8 else ops.FORMAT_RAW
-        self._engine = _CopyEngine(cache, self._layout, fmt, split_streams)
-        assert self._engine.logical_bytes == self._block_bytes
+        self._counts = Counter()
+        self._prefetched_blocks = 0  # the block manager adds its prefetches here
         self._copy_stream = self._engine.save_stream
         self._restore_stream = self._engine.restore_stream
         self._staging: list[torch.Tensor] = []
@@ -349,10 +438,9 @@ class CPUBlockCache:
                 raise RuntimeError("block manager already has an automatic CPU cache")
             block_manager._cpu_prefix_cache = self
         if preallocate:
-            while self._num_slots < self._capacity:
-                self._grow()
+            self._slots.reserve_all()
 
-    # -- properties (cpu_prefix_cache.py:133-193) --------------------------
+    # -- the reference's public surface (cpu_prefix_cache.py:133-197) -----------
 
     @property
     def max_bytes(self) -> int:
@@ -360,15 +448,15 @@ class CPUBlockCache:
 
     @property
     def block_bytes(self) -> int:
-        return self._block_bytes
+        return self._slots.entry_bytes
 
     @property
     def bytes_used(self) -> int:
-        return len(self._entries) * self._block_bytes
+        return len(self._entries) * self._slots.entry_bytes
 
     @property
     def reserved_bytes(self) -> int:
-        return self._num_slots * self._block_bytes
+        return self._slots.count * self._slots.entry_bytes
 
     @property
     def closed(self) -> bool:
@@ -376,7 +464,7 @@ class CPUBlockCache:
 
     @property
     def automatic(self) -> bool:
-        return not self.closed and self._manager._cpu_prefix_cache is self
+        return self._manager is not None and self._manager._cpu_prefix_cache is self
 
     @property
     def prefetch_enabled(self) -> bool:
@@ -388,13 +476,11 @@ class CPUBlockCache:
 
     @hybrid.setter
     def hybrid(self, costs: tuple[float, float, float] | None):
-        """Set split-admission costs, e.g. after measure_restore_s_per_block()."""
+        """Set or clear the split-admission costs, e.g. from measure_restore_s_per_block()."""
         if costs is not None:
             if not self.automatic:
                 raise ValueError("hybrid requires an automatic cache")
-            if len(costs) != 3 or min(costs) < 0:
-                raise ValueError("hybrid needs three nonnegative cost coefficients")
-            costs = tuple(float(c) for c in costs)
+            costs = _checked_costs(costs)
         self._hybrid = costs
 
     @property
@@ -407,8 +493,7 @@ class CPUBlockCache:
 
     @property
     def stats(self) -> dict[str, int]:
-        return {"saved_blocks": self._saved_blocks, "restored_blocks": self._restored_blocks,
-                "budget_skips": self._budget_skips}
+        return {name: self._counts[name] for name in ("saved_blocks", "restored_blocks", "budget_skips")}
 
     def __len__(self):
         return len(self._entries)
@@ -420,35 +505,29 @@ class CPUBlockCache:
         if self.closed:
             raise RuntimeError("CPU prefix cache is closed")
 
-    # -- host slabs and device staging -------------------------------------
+    # Views the reference's tests inspect: typed payload slabs, the pinned
+    # allocations, the free-slot stack and one slot's (payload, scale).
 
-    def _grow(self):
-        """Pin one more chunk of slots (cpu_prefix_cache.py:199-208); LIFO free list, lowest slot first."""
-        count = min(max(1, _SLAB_CHUNK_BYTES // self._block_bytes), self._capacity - self._num_slots)
-        stride = self._engine.entry_stride
-        memory = torch.empty(count * stride, dtype=torch.uint8, device="cpu", pin_memory=True)
-        rows = memory.view(count, stride)
-        payload_bytes = prod(self._shape) * self._dtype.itemsize
-        payload = rows[:, :payload_bytes].view(self._dtype).view(count, *self._shape)
-        scale = None
-        if self._fp8:
-            offset = self._engine.scale_offset
-            nbytes = prod(self._scale_shape) * self._scale_dtype.itemsize
-            scale = rows[:, offset:offset + nbytes].view(self._scale_dtype).view(count, *self._scale_shape)
-        self._engine.add_slab(memory, count)
-        self._slab_memory.append(memory)
-        self._slabs.append(payload)
-        if scale is not None:
-            self._scale_slabs.append(scale)
-        self._free_slots.extend(range(self._num_slots + count - 1, self._num_slots - 1, -1))
-        self._num_slots += count
+    @property
+    def _slabs(self) -> list[torch.Tensor]:
+        return self._slots.kv_views
+
+    @property
+    def _scale_slabs(self) -> list[torch.Tensor]:
+        return self._slots.scale_views
+
+    @property
+    def _slab_memory(self) -> list[torch.Tensor]:
+        return self._slots.memory
+
+    @property
+    def _free_slots(self) -> list[int]:
+        return self._slots.free
 
     def _slot_view(self, slot: int) -> tuple[torch.Tensor, torch.Tensor | None]:
-        for i, slab in enumerate(self._slabs):
-            if slot < len(slab):
-                return slab[slot], self._scale_slabs[i][slot] if self._fp8 else None
-            slot -= len(slab)
-        raise IndexError(slot)
+        return self._slots.view(slot)
+
+    # -- device staging and the copy seams ---------------------------------
 
     def _ensure_staging(self):
         if self._staging:
@@ -466,7 +545,41 @@ class CPUBlockCache:
     def _compute_stream(self) -> int:
         return torch.cuda.current_stream(self._cache.device).cuda_stream
 
-    # -- copies -------------------------------------------------------------
+    def _save_to_slot(self, block_id: int, slot: int):
+        """Queue pool block -> host slot on the save stream (the seam failure-injection tests patch)."""
+        self._ensure_staging()
+        self._batcher.save(block_id, slot)
+
+    def _restore_from_slot(self, slot: int, block_id: int, wait: bool):
+        """Queue host slot -> pool block on the restore stream."""
+        self._ensure_staging()
+        self._batcher.restore(slot, block_id, wait)
+
+    def coalesce(self):
+        """Batch the saves and restores issued inside a `with` block (see _CopyBatcher); used by the block
+        manager's admission, prefetch and release loops."""
+        return self._batcher.coalesce()
+
+    def _withdraw_copies(self, saves, restores):
+        """A batch of held-back copies failed to issue: drop the CPU entries its saves published and unpublish
+        the GPU blocks its restores filled, so no metadata names bytes that may never have been copied."""
+        slots = {slot for _, slot in saves}
+        for prefix_hash in [h for h, e in self._entries.items() if e.slot in slots]:
+            self._slots.give_back(self._entries.pop(prefix_hash).slot)
+            self._counts["saved_blocks"] -= 1
+        manager = self._manager
+        for _, block_id, _ in restores:
+            block = manager.blocks[block_id]
+            if block.hash != -1 and manager.hash_to_block_id.get(block.hash) == block_id:
+                del manager.hash_to_block_id[block.hash]
+            block.hash, block.token_ids = -1, []
+            self._counts["restored_blocks"] -= 1
+
+    def synchronize(self):
+        """Wait for every pending host<->device copy (needed before host reads)."""
+        if not self.closed:
+            self._batcher.flush()
+            self._engine.synchronize()
 
     def measure_restore_s_per_block(self, repeats: int = 8) -> float:
         """Time this cache's restore path (H2D DMA plus FP8 dequantisation) on scratch buffers.
@@ -503,95 +616,72 @@ class CPUBlockCache:
         finally:
             engine.close()
 
-    def synchronize(self):
-        """Wait for every pending host<->device copy (needed before host reads)."""
-        if not self.closed:
-            self._batcher.flush()
-            self._engine.synchronize()
+    # -- saving -------------------------------------------------------------
 
-    def _save_to_slot(self, block_id: int, slot: int):
-        """Queue pool block -> host slot on the save stream (the seam failure-injection tests patch)."""
-        self._ensure_staging()
-        self._batcher.save(block_id, slot)
-
-    def _restore_from_slot(self, slot: int, block_id: int, wait: bool):
-        """Queue host slot -> pool block on the restore stream."""
-        self._ensure_staging()
-        self._batcher.restore(slot, block_id, wait)
-
-    def coalesce(self):
-        """Batch the saves and restores issued inside a `with` block (see _CopyBatcher); used by the block
-        manager's admission, prefetch and release loops."""
-        return self._batcher.coalesce()
-
-    def _withdraw_copies(self, saves, restores):
-        """A batch of held-back copies failed to issue: drop the CPU entries its saves published and unpublish
-        the GPU blocks its restores filled, so no metadata names bytes that may never have been copied."""
-        slots = {slot for _, slot in saves}
-        for prefix_hash in [h for h, e in self._entries.items() if e.slot in slots]:
-            self._free_slots.append(self._entries.pop(prefix_hash).slot)
-            self._saved_blocks -= 1
-        manager = self._manager
-        for _, block_id, _ in restores:
-            block = manager.blocks[block_id]
-            if block.hash != -1 and manager.hash_to_block_id.get(block.hash) == block_id:
-                del manager.hash_to_block_id[block.hash]
-            block.hash, block.token_ids = -1, []
-            self._restored_blocks -= 1
-
-    def save_block(self, prefix_hash: int) -> bool:
-        """Save a published full block; return False if already saved (cpu_prefix_cache.py:275-332).
-
-        A full budget raises CPUCacheFullError before any allocation. A copy
-        or allocation failure leaves CPU entries and GPU metadata unchanged.
-        Partial tails cannot be saved.
-        """
-        self._require_open()
-        entry = self._entries.get(prefix_hash)
+    def _published_source(self, prefix_hash: int) -> tuple[int, tuple[int, ...]] | None:
+        """(block id, tokens) of the full GPU block published under `prefix_hash`; None if no GPU block has
+        the hash. A block holding the hash but not published with all its tokens cannot be a source."""
         block_id = self._manager.hash_to_block_id.get(prefix_hash)
         if block_id is None:
-            if entry is not None:
-                return False
-            raise KeyError(f"GPU prefix block {prefix_hash} is not cached")
+            return None
         block = self._manager.blocks[block_id]
         tokens = tuple(block.token_ids)
         if block.hash != prefix_hash or len(tokens) != self._manager.block_size:
             raise ValueError("source must be a published full prefix block")
-        if entry is not None:
-            if entry.token_ids != tokens:
+        return block_id, tokens
+
+    def save_block(self, prefix_hash: int) -> bool:
+        """Copy a published full GPU block into a host slot; False if it is saved already (:275-332).
+
+        Errors, before anything changes: KeyError if the hash is neither on
+        the GPU nor saved, ValueError for an unpublished or partial source or
+        a saved entry with other tokens, CPUCacheFullError when the budget
+        is spent. If queueing the copy fails, the slot goes back and no
+        entry appears.
+        """
+        self._require_open()
+        saved = self._entries.get(prefix_hash)
+        source = self._published_source(prefix_hash)
+        if source is None:
+            if saved is None:
+                raise KeyError(f"GPU prefix block {prefix_hash} is not cached")
+            return False
+        block_id, tokens = source
+        if saved is not None:
+            if saved.token_ids != tokens:
                 raise ValueError("prefix hash has conflicting token metadata")
             return False
-        if self.bytes_used + self.block_bytes > self.max_bytes:
+        if len(self._entries) >= self._slots.capacity:
             raise CPUCacheFullError("CPU prefix cache payload budget exceeded")
-        if not self._free_slots:
-            self._grow()
-        slot = self._free_slots.pop()
+        slot = self._slots.take()
         try:
-            payload, scale = self._slot_view(slot)
             self._save_to_slot(block_id, slot)
         except BaseException:
-            self._free_slots.append(slot)
+            self._slots.give_back(slot)
             raise
-        self._entries[prefix_hash] = _CPUBlock(tokens, payload, slot, scale, True)
-        self._saved_blocks += 1
+        kv, scale = self._slots.view(slot)
+        self._entries[prefix_hash] = _CPUBlock(tokens, kv, slot, scale, True)
+        self._counts["saved_blocks"] += 1
         return True
 
     def _preserve(self, prefix_hash: int):
-        # Only a budget miss is an expected fallback; device and allocation
-        # failures stay visible (cpu_prefix_cache.py:334-340).
+        """A save the block manager asks for: a spent budget is counted and skipped (:334-340); any other
+        failure propagates, so device errors stay visible."""
         try:
             self.save_block(prefix_hash)
         except CPUCacheFullError:
-            self._budget_skips += 1
+            self._counts["budget_skips"] += 1
 
     def _preserve_before_recycle(self, prefix_hash: int):
         self._preserve(prefix_hash)
 
     def _preserve_on_release(self, prefix_hash: int):
-        # Only when a request is waiting for blocks: otherwise the block likely
-        # stays a GPU hit and the D2H traffic would only delay later copies.
+        # Saved on release only while an admission waits for blocks: otherwise
+        # the block probably stays a GPU hit and the D2H copy buys nothing.
         if self._save_on_release and self._manager.admission_blocked:
             self._preserve(prefix_hash)
+
+    # -- restoring and ordering ---------------------------------------------
 
     def before_block_reuse(self, block_id: int):
         """Order later writes to a GPU block after its pending save and restore, without a host sync."""
@@ -602,70 +692,69 @@ class CPUBlockCache:
         self._batcher.before_block_use(block_id)
 
     def _entry_for(self, prefix_hash: int, token_ids):
-        """Pure lookup used while planning admission."""
-        entry = self._entries.get(prefix_hash)
-        return entry if entry is not None and entry.token_ids == tuple(token_ids) else None
+        """The entry saved under `prefix_hash` for exactly these tokens, else None (a lookup, no side effects)."""
+        saved = self._entries.get(prefix_hash)
+        if saved is None or saved.token_ids != tuple(token_ids):
+            return None
+        return saved
 
     def _copy_entry(self, entry: _CPUBlock, block_id: int, wait: bool = True):
-        """Restore `entry` into GPU block `block_id` (cpu_prefix_cache.py:370-398).
+        """Restore `entry` into GPU block `block_id` (:370-398).
 
         With wait=True the current stream waits for the copy; otherwise the
         block stays pending until before_block_use/before_block_reuse.
         """
         self._require_open()
         self._restore_from_slot(entry.slot, block_id, wait)
-        self._restored_blocks += 1
+        self._counts["restored_blocks"] += 1
 
     def restore_block(self, prefix_hash: int) -> int:
-        """Restore a CPU hit; return the GPU cache's physical block ID (cpu_prefix_cache.py:400-414).
+        """Restore a CPU hit into the pool and return its GPU block id (:400-414).
 
-        GPU hits are reused without copying. On copy failure the destination
-        is freed and the hash stays unpublished; the CPU entry remains for a
-        retry.
+        An existing GPU hit is returned without a copy. If the copy fails,
+        the destination is freed and stays unpublished, and the CPU entry is
+        kept for a retry.
         """
         self._require_open()
         entry = self._entries[prefix_hash]
+        return self._manager.restore_cached_block(
+            prefix_hash, entry.token_ids, lambda block_id: self._copy_entry(entry, block_id))
 
-        def copy_to_block(block_id):
-            self._copy_entry(entry, block_id)
-
-        return self._manager.restore_cached_block(prefix_hash, entry.token_ids, copy_to_block)
+    # -- releasing ----------------------------------------------------------
 
     def discard(self, prefix_hash: int) -> bool:
-        """Release one CPU payload without changing GPU cache state.
+        """Drop one CPU entry (GPU state is untouched); False if none was saved under the hash.
 
         A later save into the freed slot is ordered after restores still
         reading it by the copy engine's per-slot events.
         """
         self._require_open()
         entry = self._entries.pop(prefix_hash, None)
-        if entry is None:
-            return False
-        self._free_slots.append(entry.slot)
-        return True
+        if entry is not None:
+            self._slots.give_back(entry.slot)
+        return entry is not None
 
     def clear(self):
+        """Drop every CPU entry; the slots stay pinned for later saves."""
         for entry in self._entries.values():
-            self._free_slots.append(entry.slot)
+            self._slots.give_back(entry.slot)
         self._entries.clear()
 
     def close(self):
-        """Release payloads, streams and pool references; idempotent."""
+        """Finish pending copies, detach from the block manager and release every host and device buffer.
+
+        Idempotent; any later call but close raises RuntimeError.
+        """
         if self.closed:
             return
         if self.automatic:
             self._manager._cpu_prefix_cache = None
         self.synchronize()
-        self.clear()
+        self._entries.clear()
         self._engine.close()
         self._staging.clear()
-        self._slabs.clear()
-        self._scale_slabs.clear()
-        self._slab_memory.clear()
-        self._free_slots.clear()
-        self._num_slots = 0
-        self._cache = None
-        self._manager = None
+        self._slots.release()
+        self._cache = self._manager = None
 
     def __del__(self):
         engine = getattr(self, "_engine", None)
