@@ -16,40 +16,43 @@ Decode gives each running request one token and a new block when it crosses
 a block boundary, preempting the newest running request (or itself) when no
 block is free.
 
-A failure anywhere in a prefill or decode pass (a copy that raises) undoes
-the whole pass: queues, request fields and the blocks the pass took are as
-before, so the step can be retried (:130-141, 172-180).
+A pass records the inverse of each change it makes (an undo log). If
+anything in it raises (a copy, a save of a recycled block), the log is
+replayed newest first, so queues, request fields and the blocks the pass
+took are as before and the step can be retried (:130-141, 172-180).
+Preemptions and prefetches are not undone; they leave a consistent state.
 """
 
 from collections import deque
+from collections.abc import Callable
 
 from kvx.engine.block_manager import BlockManager
 from kvx.engine.sequence import Sequence, SequenceStatus
 
 
-class _PrefillUndo:
-    """What a prefill pass changed, for restoring it if the pass raises."""
+class _UndoLog:
+    """Inverse operations of one scheduling pass, replayed newest first by rewind()."""
 
-    def __init__(self, scheduler: "Scheduler"):
-        self.scheduler = scheduler
-        self.waiting = list(scheduler.waiting)
-        self.touched: list[tuple[Sequence, int, int, SequenceStatus, bool]] = []
-        self.promoted: list[Sequence] = []
+    def __init__(self):
+        self._inverse: list[Callable[[], None]] = []
 
-    def note(self, seq: Sequence):
-        self.touched.append((seq, seq.num_cached_tokens, seq.num_scheduled_tokens, seq.status,
-                             bool(seq.block_table)))
+    def push(self, inverse: Callable[[], None]):
+        self._inverse.append(inverse)
 
-    def restore(self):
-        manager = self.scheduler.block_manager
-        for seq, cached, scheduled, status, had_blocks in reversed(self.touched):
-            if seq.block_table and not had_blocks:
-                manager.deallocate(seq)
-            seq.num_cached_tokens, seq.num_scheduled_tokens, seq.status = cached, scheduled, status
-        for seq in self.promoted:
-            self.scheduler.running.remove(seq)
-        self.scheduler.waiting.clear()
-        self.scheduler.waiting.extend(self.waiting)
+    def remember(self, obj, *names: str):
+        """Restore these attributes of `obj` to their current values on rewind."""
+        old = {name: getattr(obj, name) for name in names}
+        self.push(lambda: [setattr(obj, name, value) for name, value in old.items()])
+
+    def assign(self, obj, **fields):
+        """Set attributes of `obj`, remembering their previous values."""
+        self.remember(obj, *fields)
+        for name, value in fields.items():
+            setattr(obj, name, value)
+
+    def rewind(self):
+        while self._inverse:
+            self._inverse.pop()()
 
 
 class Scheduler:
@@ -86,81 +89,114 @@ class Scheduler:
                 return batch, is_prefill
         raise RuntimeError("no request can progress: check GPU KV capacity and request lengths")
 
+    # -- prefill --------------------------------------------------------------------
+
+    def _tokens_to_prefill(self, seq: Sequence) -> tuple[int, int | None] | None:
+        """(tokens the request still has to prefill, cached blocks to admit it with), or None if it cannot be
+        admitted now.
+
+        A request without blocks is looked up (its cached prefix is skipped);
+        one that has blocks continues a chunked prefill or a split head (no
+        admission: None for the cached blocks).
+        """
+        if seq.block_table:
+            return seq.num_tokens - seq.num_cached_tokens, None
+        cached_blocks = self.block_manager.can_allocate(seq)
+        if cached_blocks < 0:
+            return None
+        return seq.num_tokens - cached_blocks * self.block_size, cached_blocks
+
     def _prefill_batch(self) -> list[Sequence]:
-        budget = self.max_num_batched_tokens
         manager = self.block_manager
+        log = _UndoLog()
         batch: list[Sequence] = []
-        used = 0
-        undo = _PrefillUndo(self)
+        room = self.max_num_batched_tokens
         try:
-            i = 0  # requests before i are split admissions whose head is already in this batch
-            while i < len(self.waiting) and len(batch) < self.max_num_seqs and used < budget:
-                seq = self.waiting[i]
-                undo.note(seq)
-                cached_blocks = None
-                if seq.block_table:  # a chunked prefill, or a split head, continues
-                    new_tokens = seq.num_tokens - seq.num_cached_tokens
-                else:
-                    cached_blocks = manager.can_allocate(seq)
-                    if cached_blocks < 0:
-                        manager.admission_blocked = True
-                        manager.prefetch(seq, reserve=len(self.running))
-                        break
-                    new_tokens = seq.num_tokens - cached_blocks * self.block_size
-                room = budget - used
-                if batch and new_tokens > room:
+            # Iterate over a snapshot: requests promoted to running leave the
+            # queue, split heads stay in it while later requests join.
+            for seq in list(self.waiting):
+                if not room or len(batch) == self.max_num_seqs:
                     break
+                log.remember(seq, "num_cached_tokens", "num_scheduled_tokens", "status")
+                fit = self._tokens_to_prefill(seq)
+                if fit is None:
+                    manager.admission_blocked = True
+                    manager.prefetch(seq, reserve=len(self.running))
+                    break
+                needed, cached_blocks = fit
+                if batch and needed > room:
+                    break  # only the first request of a batch may be chunked
                 if cached_blocks is not None:
                     manager.allocate(seq, cached_blocks)
-                stop = seq.restore_span[0] if seq.restore_span else seq.num_tokens
-                seq.num_scheduled_tokens = min(stop - seq.num_cached_tokens, room)
-                used += seq.num_scheduled_tokens
+                    log.push(lambda seq=seq: manager.deallocate(seq))
+                end = seq.restore_span[0] if seq.restore_span else seq.num_tokens
+                seq.num_scheduled_tokens = min(end - seq.num_cached_tokens, room)
+                room -= seq.num_scheduled_tokens
                 batch.append(seq)
                 reached = seq.num_cached_tokens + seq.num_scheduled_tokens
                 if reached == seq.num_tokens:
-                    seq.status = SequenceStatus.RUNNING
-                    del self.waiting[i]
-                    undo.promoted.append(seq)
-                    self.running.append(seq)
-                elif seq.restore_span and reached == seq.restore_span[0]:
-                    i += 1
-                else:
+                    self._promote(seq, log)
+                elif not (seq.restore_span and reached == seq.restore_span[0]):
                     break  # chunked: it stays at the head of the queue
         except BaseException:
-            undo.restore()
+            log.rewind()
             raise
         return batch
 
+    def _promote(self, seq: Sequence, log: _UndoLog):
+        """The request's whole prompt is in this batch: it moves from waiting to running."""
+        position = self.waiting.index(seq)
+        del self.waiting[position]
+        self.running.append(seq)
+        seq.status = SequenceStatus.RUNNING
+
+        def undo():
+            self.running.remove(seq)
+            self.waiting.insert(position, seq)
+
+        log.push(undo)
+
+    # -- decode -----------------------------------------------------------------------
+
+    def _make_room(self, seq: Sequence) -> bool:
+        """Preempt the newest running requests until `seq` can grow; False if `seq` itself had to go."""
+        manager = self.block_manager
+        while not manager.can_append(seq):
+            if not self.running:
+                self.preempt(seq)
+                return False
+            self.preempt(self.running.pop())
+        return True
+
     def _decode_batch(self) -> list[Sequence]:
         manager = self.block_manager
+        log = _UndoLog()
         batch: list[Sequence] = []
-        before: list[tuple[Sequence, int, int, bool]] = []  # state of each request this pass grew
+        popped: list[Sequence] = []
         try:
             while self.running and len(batch) < self.max_num_seqs:
                 seq = self.running.popleft()
-                while seq is not None and not manager.can_append(seq):
-                    if self.running:
-                        self.preempt(self.running.pop())
-                    else:
-                        self.preempt(seq)
-                        seq = None
-                if seq is None:
+                popped.append(seq)
+                if not self._make_room(seq):
                     continue
-                before.append((seq, len(seq.block_table), seq.num_scheduled_tokens, seq.is_prefill))
-                seq.num_scheduled_tokens = 1
-                seq.is_prefill = False
+                log.assign(seq, num_scheduled_tokens=1, is_prefill=False)
+                length = len(seq.block_table)
+                log.push(lambda seq=seq, length=length: self._shrink(seq, length))
                 manager.may_append(seq)
                 batch.append(seq)
         except BaseException:
-            for seq, length, scheduled, was_prefill in reversed(before):
-                for block_id in reversed(seq.block_table[length:]):
-                    manager._release_block(block_id)
-                del seq.block_table[length:]
-                seq.num_scheduled_tokens, seq.is_prefill = scheduled, was_prefill
-            self.running.extendleft(reversed([seq for seq, *_ in before]))
+            log.rewind()
+            # Requests taken off the queue go back to its front in order, unless preempted.
+            self.running.extendleft(reversed([seq for seq in popped if seq.status is not SequenceStatus.WAITING]))
             raise
         self.running.extendleft(reversed(batch))
         return batch
+
+    def _shrink(self, seq: Sequence, length: int):
+        """Give back the blocks `seq` gained beyond its first `length`."""
+        for block_id in reversed(seq.block_table[length:]):
+            self.block_manager._release_block(block_id)
+        del seq.block_table[length:]
 
     def preempt(self, seq: Sequence):
         """Back to the front of the waiting queue without its KV (it is recomputed or hit again)."""
@@ -169,20 +205,29 @@ class Scheduler:
         self.block_manager.deallocate(seq)
         self.waiting.appendleft(seq)
 
+    # -- after the model ran ---------------------------------------------------------------
+
     def postprocess(self, seqs: list[Sequence], token_ids: list[int], is_prefill: bool):
-        """After the model ran: publish filled blocks, advance, append sampled tokens, retire finished requests."""
-        manager = self.block_manager
+        """Publish filled blocks, advance, append sampled tokens and retire finished requests."""
         for seq, token_id in zip(seqs, token_ids):
-            manager.hash_blocks(seq)
-            seq.num_cached_tokens += seq.num_scheduled_tokens
-            seq.num_scheduled_tokens = 0
-            if seq.restore_span and seq.num_cached_tokens == seq.restore_span[0]:
-                manager.finish_restore_span(seq)
+            self._advance(seq)
             if is_prefill and seq.num_cached_tokens < seq.num_tokens:
                 continue  # a chunk or a split head: no token is sampled yet
-            seq.append_token(token_id)
-            hit_eos = not seq.ignore_eos and token_id == self.eos
-            if hit_eos or seq.num_completion_tokens == seq.max_tokens:
-                seq.status = SequenceStatus.FINISHED
-                manager.deallocate(seq)
-                self.running.remove(seq)
+            self._sample(seq, token_id)
+
+    def _advance(self, seq: Sequence):
+        """The step's tokens now have KV: publish the blocks they fill, and skip a restored span once reached."""
+        manager = self.block_manager
+        manager.hash_blocks(seq)
+        seq.num_cached_tokens += seq.num_scheduled_tokens
+        seq.num_scheduled_tokens = 0
+        if seq.restore_span and seq.num_cached_tokens == seq.restore_span[0]:
+            manager.finish_restore_span(seq)
+
+    def _sample(self, seq: Sequence, token_id: int):
+        seq.append_token(token_id)
+        stop = token_id == self.eos and not seq.ignore_eos
+        if stop or seq.num_completion_tokens == seq.max_tokens:
+            seq.status = SequenceStatus.FINISHED
+            self.block_manager.deallocate(seq)
+            self.running.remove(seq)

@@ -297,7 +297,8 @@ def test_prefetch_uses_spare_blocks_once_and_marks_them_pending():
     copies = [c for c in cache.calls if c[0] == "copy"]
     assert all(wait is False for *_, wait in copies) and cache._prefetched_blocks == 2
     assert all(k in manager.hash_to_block_id for k in keys)
-    assert manager._protected == {manager.hash_to_block_id[k] for k in keys}
+    # LRU keeps the prefetched blocks from recycling by their place: the back of the free order.
+    assert list(manager.free_block_ids)[-2:] == [manager.hash_to_block_id[k] for k in keys]
     consistent(manager)
     cache.prefetch_enabled = False
     assert manager.prefetch(Sequence([1] * 600, params())) == 0
