@@ -5,6 +5,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <initializer_list>
 #include <mutex>
 #include <new>
 #include <utility>
@@ -29,6 +30,33 @@ int hip_status(hipError_t err, const char* what) {
   return set_error((int)err, "%s: %s (hipError_t %d)", what, hipGetErrorString(err), (int)err);
 }
 
+// No layout, tensor, entry run or slab this library addresses may span more
+// than this many bytes (1 TiB, above any MI355X pool or host slab). Every size
+// the kernels and the entry sizing compute then fits int64 with room to spare.
+constexpr int64_t kMaxSpan = int64_t{1} << 40;
+
+// *out = the product of `factors`; false if a factor is negative or the
+// product overflows or exceeds kMaxSpan.
+static bool span_product(std::initializer_list<int64_t> factors, int64_t* out) {
+  int64_t p = 1;
+  for (int64_t f : factors)
+    if (f < 0 || __builtin_mul_overflow(p, f, &p) || p > kMaxSpan) return false;
+  *out = p;
+  return true;
+}
+
+// Bytes from the first element of a strided run of `count` rows of `row`
+// elements (rows `stride` elements apart) to the end of its last row, or -1 if
+// that is more than kMaxSpan bytes.
+static int64_t strided_span(int64_t count, int64_t stride, int64_t row, int64_t elem_bytes) {
+  int64_t lead, elems, bytes;
+  if (count <= 0) return 0;
+  if (__builtin_mul_overflow(count - 1, stride, &lead) || __builtin_add_overflow(lead, row, &elems) ||
+      !span_product({elems, elem_bytes}, &bytes))
+    return -1;
+  return bytes;
+}
+
 int check_layout(const kvx_block_layout* l, int32_t format) {
   if (!l) return set_error(KVX_E_INVALID, "layout is NULL");
   if (format != KVX_FORMAT_RAW && format != KVX_FORMAT_FP8)
@@ -49,6 +77,17 @@ int check_layout(const kvx_block_layout* l, int32_t format) {
   } else if (l->elem_bytes != 1 && l->elem_bytes != 2 && l->elem_bytes != 4 && l->elem_bytes != 8) {
     return set_error(KVX_E_INVALID, "elem_bytes must be 1, 2, 4 or 8");
   }
+  int64_t block_bytes;
+  if (!span_product({l->planes, l->plane_rows, l->head_dim, l->elem_bytes}, &block_bytes))
+    return set_error(KVX_E_UNSUPPORTED, "a block of this layout spans more than 2^40 bytes");
+  // The pool the layout describes ends with the last plane of the last block.
+  int64_t blocks_lead, planes_lead, extent_elems, extent_bytes;
+  if (__builtin_mul_overflow((int64_t)l->num_blocks - 1, l->block_stride, &blocks_lead) ||
+      __builtin_mul_overflow((int64_t)l->planes - 1, l->plane_stride, &planes_lead) ||
+      __builtin_add_overflow(blocks_lead, planes_lead, &extent_elems) ||
+      __builtin_add_overflow(extent_elems, plane_elems, &extent_elems) ||
+      !span_product({extent_elems, l->elem_bytes}, &extent_bytes))
+    return set_error(KVX_E_UNSUPPORTED, "the layout spans more than 2^40 bytes");
   // Launch grids: blocks * planes * tiles must fit a 32-bit workgroup count.
   if ((int64_t)kMaxBatch * l->planes * ((plane_elems * l->elem_bytes) / 16 + 1) > (int64_t)INT32_MAX)
     return set_error(KVX_E_UNSUPPORTED, "block geometry too large for one launch");
@@ -163,6 +202,9 @@ static int token_copy(bool gather, void* pool, const kvx_block_layout* l, const 
   if (num_rows == 0) return KVX_OK;
   if (!pool || !dense || !table) return set_error(KVX_E_INVALID, "NULL pool, buffer or block table");
   if ((uintptr_t)pool % 2 || (uintptr_t)dense % 2) return set_error(KVX_E_INVALID, "buffers must be 2-byte aligned");
+  int64_t dense_bytes;
+  if (!span_product({l->planes, num_rows, l->head_dim, l->elem_bytes}, &dense_bytes))
+    return set_error(KVX_E_UNSUPPORTED, "%lld rows span more than 2^40 bytes", (long long)num_rows);
   const int64_t row_bytes = (int64_t)l->head_dim * l->elem_bytes;
   const int64_t plane_bytes = (int64_t)l->plane_rows * row_bytes;
   const int64_t nblocks = (num_rows + l->plane_rows - 1) / l->plane_rows;
@@ -203,6 +245,10 @@ static int token_fp8(bool gather, void* pool, const kvx_block_layout* l, const i
   const int64_t sb = l->scale_dtype == KVX_SCALE_BF16 ? 2 : 4;
   if ((uintptr_t)pool % 2) return set_error(KVX_E_INVALID, "pool is not 2-byte aligned");
   if ((uintptr_t)scales % (uintptr_t)sb) return set_error(KVX_E_INVALID, "scales are not %lld-byte aligned", (long long)sb);
+  int64_t payload_span, scale_span;
+  if (!span_product({l->planes, num_rows, l->head_dim}, &payload_span) ||
+      !span_product({l->planes, num_rows, sb}, &scale_span))
+    return set_error(KVX_E_UNSUPPORTED, "%lld rows span more than 2^40 bytes", (long long)num_rows);
   const int64_t R = l->plane_rows, hd = l->head_dim;
   const int64_t nblocks = (num_rows + R - 1) / R;
   if (nblocks > table_len)
@@ -696,6 +742,11 @@ int kvx_store_kvcache(const void* key, int64_t key_stride, const void* value, in
     return set_error(KVX_E_INVALID, "NULL tensor pointer");
   if (num_tokens > (int64_t)INT32_MAX) return set_error(KVX_E_UNSUPPORTED, "too many tokens for one launch");
   const int64_t row = (int64_t)num_heads * head_dim;
+  int64_t cache_bytes;
+  if (strided_span(num_tokens, key_stride, row, elem_bytes) < 0 ||
+      strided_span(num_tokens, value_stride, row, elem_bytes) < 0 ||
+      !span_product({cache_slots, row, elem_bytes}, &cache_bytes))
+    return set_error(KVX_E_UNSUPPORTED, "key, value or cache spans more than 2^40 bytes");
   hipError_t err = launch_store_kvcache(key, key_stride, value, value_stride, k_cache, v_cache, slot_mapping,
                                         num_tokens, row, elem_bytes, cache_slots, (hipStream_t)stream);
   return hip_status(err, "store_kvcache launch");
@@ -818,6 +869,9 @@ int kvx_cache_set_staging(kvx_cache* c, void* save_staging, void* restore_stagin
     return set_error(KVX_E_INVALID, "staging buffers must be 256-byte aligned");
   if (!c->split && save_staging != restore_staging)
     return set_error(KVX_E_INVALID, "one stream shares one staging buffer");
+  int64_t staging_bytes;
+  if (!span_product({entries, c->entry_stride}, &staging_bytes))
+    return set_error(KVX_E_UNSUPPORTED, "staging of %d entries spans more than 2^40 bytes", entries);
   c->save_staging = (uint8_t*)save_staging;
   c->restore_staging = (uint8_t*)restore_staging;
   c->staging_entries = entries;
@@ -829,6 +883,9 @@ int kvx_cache_add_slab(kvx_cache* c, void* host_base, int32_t count) {
   if (!host_base || count <= 0) return set_error(KVX_E_INVALID, "slab needs memory and a positive slot count");
   if ((uintptr_t)host_base % 256) return set_error(KVX_E_INVALID, "slab must be 256-byte aligned");
   if ((int64_t)c->num_slots + count > (int64_t)INT32_MAX) return set_error(KVX_E_RANGE, "too many slots");
+  int64_t slab_bytes;
+  if (!span_product({count, c->entry_stride}, &slab_bytes))
+    return set_error(KVX_E_UNSUPPORTED, "a slab of %d entries spans more than 2^40 bytes", count);
   c->slabs.push_back(Slab{(uint8_t*)host_base, c->num_slots, count});
   c->num_slots += count;
   c->slot_read.resize(c->num_slots, nullptr);

@@ -9,6 +9,7 @@ from types import SimpleNamespace
 
 import pytest
 import torch
+from hypothesis import example, given, settings, strategies as st
 
 from kvx import _lib, ops
 from kvx.engine.block_manager import BlockManager
@@ -173,3 +174,88 @@ def test_a_missing_library_fails_loudly(monkeypatch):
     layout = ops.pool_layout(torch.zeros((2, 1, 2, 4, 1, 8), dtype=torch.bfloat16))
     with pytest.raises(RuntimeError, match="libkvx is not built"):
         ops.entry_layout(layout, ops.FORMAT_FP8)
+
+
+# -- layout and size validation: exact arithmetic against the library's answer ----------
+
+_SPAN = 1 << 40
+_INT32 = st.one_of(st.integers(-2, 300), st.integers(0, 2**31 - 1))
+_INT64 = st.one_of(st.integers(-2, 1 << 20), st.integers(0, 2**63 - 1))
+
+
+def _ceil256(n: int) -> int:
+    return -(-n // 256) * 256
+
+
+def _layout_accepted(fmt, planes, rows, hd, blocks, plane_stride, block_stride, elem, scale) -> bool:
+    """What the library must accept, in Python integers (no overflow)."""
+    if fmt not in (ops.FORMAT_RAW, ops.FORMAT_FP8) or min(planes, rows, hd, blocks) <= 0:
+        return False
+    if plane_stride < 0 or block_stride < 0 or (blocks > 1 and block_stride < rows * hd):
+        return False
+    if fmt == ops.FORMAT_FP8 and (elem != 2 or scale not in (0, 1)):
+        return False
+    if fmt == ops.FORMAT_RAW and elem not in (1, 2, 4, 8):
+        return False
+    if planes * rows * hd * elem > _SPAN:
+        return False
+    if ((blocks - 1) * block_stride + (planes - 1) * plane_stride + rows * hd) * elem > _SPAN:
+        return False
+    return 128 * planes * ((rows * hd * elem) // 16 + 1) <= 2**31 - 1
+
+
+@settings(max_examples=600, deadline=None)
+# Boundary cases random generation rarely reaches: a pool extent of exactly 2^40 bytes and one byte more,
+# strides whose products overflow int64, and dimensions whose byte count wraps int64.
+@example(fmt=ops.FORMAT_RAW, planes=1, rows=1, hd=16, blocks=2, plane_stride=0, block_stride=2**40 - 16, elem=1,
+         scale=0)
+@example(fmt=ops.FORMAT_RAW, planes=1, rows=1, hd=16, blocks=2, plane_stride=0, block_stride=2**40 - 15, elem=1,
+         scale=0)
+@example(fmt=ops.FORMAT_FP8, planes=72, rows=2048, hd=128, blocks=2, plane_stride=2**20, block_stride=2**62,
+         elem=2, scale=1)
+@example(fmt=ops.FORMAT_FP8, planes=2, rows=2048, hd=128, blocks=1, plane_stride=2**63 - 1, block_stride=0,
+         elem=2, scale=0)
+@example(fmt=ops.FORMAT_RAW, planes=1, rows=2**31 - 1, hd=2**31 - 1, blocks=1, plane_stride=0, block_stride=0,
+         elem=8, scale=0)
+@given(fmt=st.sampled_from([ops.FORMAT_RAW, ops.FORMAT_FP8, 7]), planes=_INT32, rows=_INT32, hd=_INT32,
+       blocks=_INT32, plane_stride=_INT64, block_stride=_INT64, elem=st.sampled_from([1, 2, 3, 4, 8]),
+       scale=st.sampled_from([0, 1, 5]))
+def test_entry_layout_accepts_exactly_the_valid_layouts_and_sizes_them(fmt, planes, rows, hd, blocks, plane_stride,
+                                                                       block_stride, elem, scale):
+    layout = _lib.BlockLayout(plane_stride, block_stride, planes, rows, hd, blocks, elem, scale)
+    logical, offset, stride = ctypes.c_int64(-1), ctypes.c_int64(-1), ctypes.c_int64(-1)
+    rc = _lib.lib().kvx_entry_layout(ctypes.byref(layout), fmt, ctypes.byref(logical), ctypes.byref(offset),
+                                     ctypes.byref(stride))
+    accepted = _layout_accepted(fmt, planes, rows, hd, blocks, plane_stride, block_stride, elem, scale)
+    assert (rc == 0) == accepted, (rc, _lib.lib().kvx_last_error())
+    if not accepted:
+        assert rc in (_lib.E_INVALID, _lib.E_UNSUPPORTED)
+        return
+    total_rows = planes * rows
+    if fmt == ops.FORMAT_FP8:
+        scale_bytes = total_rows * (2 if scale == 0 else 4)
+        want = (total_rows * hd + scale_bytes, _ceil256(total_rows * hd), _ceil256(_ceil256(total_rows * hd)
+                                                                                     + scale_bytes))
+    else:
+        want = (total_rows * hd * elem, 0, _ceil256(total_rows * hd * elem))
+    assert (logical.value, offset.value, stride.value) == want
+
+
+def test_spans_beyond_two_to_the_40_bytes_are_refused_before_any_device_work():
+    # These addresses are never dereferenced: each call fails in its size checks.
+    handle = _lib.lib()
+    with pytest.raises(NotImplementedError, match="2\\^40"):
+        _lib.check(handle.kvx_store_kvcache(16, 1 << 61, 16, 0, 16, 16, 16, 3, 8, 128, 2, 10, None))
+    with pytest.raises(NotImplementedError, match="2\\^40"):
+        _lib.check(handle.kvx_store_kvcache(16, 1024, 16, 1024, 16, 16, 16, 3, 8, 128, 2, 1 << 40, None))
+    layout = layout_for(QWEN3_8B_POOL, torch.float32)
+    table = _lib.int32_array([0])
+    with pytest.raises(NotImplementedError, match="2\\^40"):
+        _lib.check(handle.kvx_gather_tokens(4096, ctypes.byref(layout), table, 1, 1 << 50, 4096, None))
+    with pytest.raises(NotImplementedError, match="2\\^40"):
+        _lib.check(handle.kvx_gather_tokens_fp8(4096, ctypes.byref(layout), table, 1, 1 << 50, 4096, 8192, None))
+    wide = layout_for(QWEN3_8B_POOL, torch.float32)
+    wide.block_stride = 1 << 62
+    with pytest.raises(NotImplementedError, match="2\\^40"):
+        _lib.check(handle.kvx_restore_blocks(4096, ctypes.byref(wide), ops.FORMAT_FP8, table,
+                                             _lib.uint64_array([4096]), 1, 0, None))
