@@ -26,6 +26,7 @@ import argparse
 import ctypes
 import json
 import os
+import subprocess
 import sys
 import time
 from contextlib import contextmanager
@@ -957,8 +958,20 @@ def host_inventory(torch):
     except OSError:
         pass
     usable = affinity if quota is None else max(1, min(affinity, int(quota)))
+
+    def command(*argv):
+        try:
+            return subprocess.run(argv, capture_output=True, text=True, timeout=10, check=True).stdout
+        except (OSError, subprocess.SubprocessError):
+            return ""
+
+    lscpu = {k.strip(): v.strip() for k, _, v in (line.partition(":") for line in command("lscpu").splitlines())}
+    nproc = command("nproc").strip()
     bdf = gpu_pci_address(0)
-    return {"nproc": os.cpu_count(), "affinity_cpus": affinity, "cgroup_cpu_quota": quota, "cpu_model": model,
+    return {"nproc": int(nproc) if nproc.isdigit() else None, "os_cpu_count": os.cpu_count(),
+            "affinity_cpus": affinity, "cgroup_cpu_quota": quota, "cpu_model": model,
+            "lscpu_model": lscpu.get("Model name"), "lscpu_cpus": lscpu.get("CPU(s)"),
+            "lscpu_sockets": lscpu.get("Socket(s)"),
             "usable_cpus": usable, "torch_threads_default": torch.get_num_threads(),
             "omp_num_threads": os.environ.get("OMP_NUM_THREADS"), "gpu": torch.cuda.get_device_name(0),
             "gpu_pci": bdf, "pcie_path": pcie_path(bdf)}
@@ -1271,6 +1284,11 @@ def cpu_baseline_leg(torch, pool, sources, dests, scale_dtype, inventory, pairs=
         "fp8_qwen3_0_6b_16_blocks": {"save_s": round(c1_save, 4), "restore_s": round(c1_restore, 4),
                                      "logical_kv_gbs": logical(32, small_block, c1_save + c1_restore)},
         "threads_basis": "sched_getaffinity capped by the cgroup CPU quota",
+        "torch_threads": torch.get_num_threads(),
+        "host": {key: inventory.get(key) for key in ("nproc", "affinity_cpus", "cgroup_cpu_quota", "cpu_model",
+                                                      "lscpu_model", "torch_threads_default", "omp_num_threads")},
+        "runs": runs,
+        "warmup_runs": 1,
     }
 
 
