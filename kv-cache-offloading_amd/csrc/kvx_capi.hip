@@ -487,6 +487,18 @@ struct kvx_cache {
     return rc;
   }
 
+  // The save kernel just queued on `s` is the last reader of these pool
+  // blocks: their pending_save becomes an event recorded now.
+  int release_blocks_after(const int32_t* ids, int32_t n, hipStream_t s) {
+    Event* read = nullptr;
+    int rc = new_event(&read);
+    if (!rc) rc = hip_status(hipEventRecord(read->ev, s), "hipEventRecord");
+    if (!rc)
+      for (int32_t i = 0; i < n; ++i) assign(pending_save[ids[i]], read);
+    if (read) release_if_unused(read);
+    return rc;
+  }
+
   // `s` waits for `e`. An event that has already completed orders nothing
   // queued from now on, so it costs no wait: a one-block restore used to
   // queue one on its slot's long-finished save.
@@ -682,7 +694,16 @@ static int save_blocks_to_slots(kvx_cache* c, const int32_t* ids, const int32_t*
       }
     }
   }
-  if (kvx_cache::direct_save(n, caller_busy)) {
+  // A staged save reads its pool blocks in the kernel; the copies to the
+  // host read only the staging. Each chunk's blocks are therefore released
+  // (pending_save) by an event right after its kernel, so a restore into a
+  // recycled victim, or the caller's writes into it, wait for the kernel and
+  // not for the transfer: the restore's host-to-device copies then overlap
+  // the save's device-to-host ones. The host slots are released (slot_saved)
+  // after the copies. A kernel-written save, and one with a fixed event (the
+  // allocation-free save, which creates none), release both after the copies.
+  const bool direct = kvx_cache::direct_save(n, caller_busy);
+  if (direct) {
     rc = c->launch(true, ids, nullptr, slots, n, s);
     if (rc) return rc;
   } else {
@@ -690,6 +711,7 @@ static int save_blocks_to_slots(kvx_cache* c, const int32_t* ids, const int32_t*
     for (int32_t base = 0; base < n; base += step) {
       const int32_t cnt = std::min(step, n - base);
       rc = c->launch(true, ids + base, staging, nullptr, cnt, s);
+      if (!rc && !fixed_done) rc = c->release_blocks_after(ids + base, cnt, s);
       if (!rc) rc = c->dma(true, staging, slots + base, cnt, s);
       if (rc) return rc;
     }
@@ -702,7 +724,7 @@ static int save_blocks_to_slots(kvx_cache* c, const int32_t* ids, const int32_t*
     return rc;
   }
   for (int32_t i = 0; i < n; ++i) {
-    c->assign(c->pending_save[ids[i]], done);
+    if (direct || fixed_done) c->assign(c->pending_save[ids[i]], done);
     c->assign(c->slot_saved[slots[i]], done);
   }
   c->assign(c->last_save, done);
@@ -954,33 +976,52 @@ int kvx_cache_restore(kvx_cache* c, const int32_t* slots, const int32_t* ids, in
   // per call on MI355X, against ~5 us for the launch.
   const bool direct = c->direct_restore(n, wait != 0);
   hipStream_t s = direct ? compute : c->restore_stream;
-  // The destination may still be read by queued kernels (cpu_prefix_cache.py:375-379).
-  rc = c->wait_stream(s, compute);
-  if (rc) return rc;
-  if (c->split || s != c->save_stream) {
-    for (int32_t i = 0; i < n; ++i) {
-      // The payload may still be arriving from its own save (:380-381).
-      Event* sv = (c->debug & KVX_DEBUG_SKIP_SAVE_WAIT) ? nullptr : c->slot_saved[slots[i]];
-      if (sv) {
-        rc = c->wait_event(s, sv);
-        if (rc) return rc;
+  // What the work of blocks [base, base + cnt) waits for on `s`. With the
+  // restore on the save stream (one copy stream), stream order covers saves.
+  const bool order_saves = c->split || s != c->save_stream;
+  // Before a copy reads the slots: their payload may still be arriving from
+  // its save (:380-381).
+  auto wait_slots = [&](int32_t base, int32_t cnt) -> int {
+    if (!order_saves || (c->debug & KVX_DEBUG_SKIP_SAVE_WAIT)) return KVX_OK;
+    for (int32_t i = base; i < base + cnt; ++i)
+      if (Event* sv = c->slot_saved[slots[i]]) {
+        const int r = c->wait_event(s, sv);
+        if (r) return r;
       }
-      // A save of the destination's previous contents may still be reading it.
-      Event* ps = (c->debug & KVX_DEBUG_SKIP_VICTIM_WAIT) ? nullptr : c->pending_save[ids[i]];
-      if (ps && ps != sv) {
-        rc = c->wait_event(s, ps);
-        if (rc) return rc;
+    return KVX_OK;
+  };
+  // Before a kernel writes the destinations: a save of a recycled victim may
+  // still be reading one (the save releases its blocks once its kernel has
+  // read them, so this does not wait for the save's transfer).
+  auto wait_victims = [&](int32_t base, int32_t cnt) -> int {
+    if (!order_saves || (c->debug & KVX_DEBUG_SKIP_VICTIM_WAIT)) return KVX_OK;
+    for (int32_t i = base; i < base + cnt; ++i) {
+      Event* ps = c->pending_save[ids[i]];
+      if (ps && ps != c->slot_saved[slots[i]]) {
+        const int r = c->wait_event(s, ps);
+        if (r) return r;
       }
     }
-  }
+    return KVX_OK;
+  };
+  // Before the first kernel: the destinations may still be read by kernels
+  // queued on the caller's stream (:375-379). The copies into staging before
+  // it touch no destination, so they start without these waits, beside the
+  // transfers of saves still in flight.
   if (direct) {
-    rc = c->launch(false, ids, nullptr, slots, n, s);
+    rc = c->wait_stream(s, compute);
+    if (!rc) rc = wait_slots(0, n);
+    if (!rc) rc = wait_victims(0, n);
+    if (!rc) rc = c->launch(false, ids, nullptr, slots, n, s);
     if (rc) return rc;
   } else {
     const int32_t step = c->chunk();
     for (int32_t base = 0; base < n; base += step) {
       const int32_t cnt = std::min(step, n - base);
-      rc = c->dma(false, c->restore_staging, slots + base, cnt, s);
+      rc = wait_slots(base, cnt);
+      if (!rc) rc = c->dma(false, c->restore_staging, slots + base, cnt, s);
+      if (!rc && base == 0) rc = c->wait_stream(s, compute);
+      if (!rc) rc = wait_victims(base, cnt);
       if (!rc) rc = c->launch(false, ids + base, c->restore_staging, nullptr, cnt, s);
       if (rc) return rc;
     }

@@ -543,6 +543,58 @@ def test_waited_restores_on_the_callers_stream_finish_before_synchronize_and_clo
         engine.close()
 
 
+def chunked_recycle(gpu, debug: int = 0) -> bool:
+    """An admission under memory pressure, batched; True if every byte comes out right.
+
+    12 victims are saved through a 4-entry staging (three chunks, each read
+    by its own kernel), then 12 entries are restored into those same blocks,
+    waited for. The saves are delayed, so every restore copy is ready long
+    before the save kernels run: each restore chunk must still wait for the
+    kernel that read its destinations, or it overwrites a victim unsaved.
+    `debug` drops ordering rules (kvx._lib.DEBUG_*) for the negative control.
+    """
+    from kvx.engine.cpu_prefix_cache import _CopyEngine
+
+    g = torch.Generator(device=gpu).manual_seed(31)
+    pool = torch.randn((2, 2, 24, BS, 8, 128), generator=g, device=gpu).to(torch.bfloat16)
+    layout = ops.pool_layout(pool, torch.float32)
+    engine = _CopyEngine(pool, layout, ops.FORMAT_FP8, split=True)
+    try:
+        stride, offset = engine.entry_stride, engine.scale_offset
+        slab = torch.full((24 * stride,), 0xAB, dtype=torch.uint8, pin_memory=True)
+        staging = [torch.empty(4 * stride, dtype=torch.uint8, device=gpu) for _ in range(2)]
+        engine.add_slab(slab, 24)
+        engine.set_staging(*staging, 4)
+        compute = torch.cuda.current_stream(gpu).cuda_stream
+        victims, others = list(range(12)), list(range(12, 24))
+        engine.save(others, others, compute)  # slots 12..23: entries of blocks 12..23
+        engine.synchronize()
+        before = bf16_bits(pool)
+        engine.set_debug(debug)
+        ops.sleep(DELAY_US, stream=engine.save_stream, device=gpu)
+        engine.save(victims, victims, compute)
+        engine.restore(others, victims, True, compute)
+        engine.synchronize()
+        torch.cuda.synchronize()
+        entries = slab.view(24, stride).numpy()
+        after = bf16_bits(pool)
+        for v, o in zip(victims, others):
+            codes, scales = oracle.save_block_fp8(before, v, True)
+            if not (np.array_equal(entries[v, :codes.size], codes.ravel())
+                    and np.array_equal(entries[v, offset:offset + scales.nbytes], scales.view(np.uint8).ravel())):
+                return False  # the victim was saved after a restore overwrote it
+            restored_codes, restored_scales = oracle.save_block_fp8(before, o, True)
+            if not np.array_equal(after[:, :, v], oracle.dequantize(restored_codes, restored_scales, True)):
+                return False
+        return np.array_equal(after[:, :, 12:], before[:, :, 12:])
+    finally:
+        engine.close()
+
+
+def test_restores_into_victims_of_a_chunked_save_wait_for_each_chunk_kernel(gpu):
+    assert chunked_recycle(gpu)
+
+
 def test_a_failed_batch_withdraws_the_metadata_it_published(gpu, monkeypatch):
     pool = make_pool(gpu, 6)
     manager = BlockManager(6, BS)

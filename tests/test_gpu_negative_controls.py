@@ -188,3 +188,9 @@ def save_without_slot_read_wait(gpu):
 
 def test_save_overwrites_a_slot_a_prefetch_still_reads_without_the_slot_read_wait(gpu):
     assert shows_race(save_without_slot_read_wait, gpu)
+
+
+def test_chunked_recycle_overwrites_victims_before_their_save_without_the_victim_wait(gpu):
+    from test_gpu_cache import chunked_recycle
+
+    assert shows_race(lambda device: not chunked_recycle(device, _lib.DEBUG_SKIP_VICTIM_WAIT), gpu)
