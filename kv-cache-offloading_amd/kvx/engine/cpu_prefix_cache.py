@@ -32,8 +32,11 @@ from kvx.engine.block_manager import BlockManager
 # call covers many entries (cpu_prefix_cache.py:11-13).
 _SLAB_CHUNK_BYTES = 1 << 30
 
-# Device staging per copy stream: entries of one save/restore batch.
-_STAGING_BYTES = 256 << 20
+# Device staging per copy stream: entries of one save/restore batch (52
+# Qwen3-8B FP8 entries). A batch larger than the staging is processed in
+# chunks, and on one stream each chunk's kernel waits for the previous
+# chunk's transfer; a larger staging reads more of a batch's blocks at once.
+_STAGING_BYTES = 1 << 30
 _MAX_BATCH = 128  # kMaxBatch in the library
 
 # The codec operators live in this module in the reference (cpu_prefix_cache.py:20-28).
@@ -172,13 +175,23 @@ class _CopyBatcher:
     for a batch, and one-block saves beside restores at ~83-86 GB/s against
     ~94. Batched saves are staged, and slowed concurrent bf16 matmuls by ~10%
     where one-block saves (written by a kernel) slowed them by 40-60%. Inside
-    coalesce() saves, restores and before_block_reuse waits
-    are held back; on exit the saves go first (one call), then the caller's
-    stream waits for the blocks passed to before_block_reuse, then the
-    restores (one call per run of equal wait flags). Restores with wait=True
-    and before_block_reuse therefore take effect at the end of the block, so
-    no work that reads or writes those blocks may be queued on the caller's
-    stream inside it. Anything that must follow a held-back copy flushes
+    coalesce() saves, restores and before_block_reuse waits are held back. On
+    exit:
+      1. the saves go first, in one call, blocks that this flush restores
+         into ahead of the others: the copy engine releases a saved block
+         once its save kernel has read it, so restores into the first
+         chunks can start while the later chunks still cross the link;
+      2. the restores, one call per run of equal wait flags;
+      3. the caller's stream waits for the blocks passed to
+         before_block_reuse, except blocks restored into here: a restore
+         waits for its destination's save itself, and the caller waits for
+         the restore (wait=True, or before_block_use) before touching the
+         block. Queued after the restores, these waits do not hold the
+         restores back (a restore waits for work on the caller's stream).
+    Restores with wait=True and before_block_reuse therefore take effect at
+    the end of the block, so no work that reads or writes those blocks may be
+    queued on the caller's stream inside it. Anything that must follow a
+    held-back copy flushes
     first: a save of a block a held-back restore writes, a save into a slot a
     held-back restore reads or a held-back save writes, a restore into a block
     a held-back restore writes, before_block_use or before_block_reuse of a
@@ -197,7 +210,7 @@ class _CopyBatcher:
         self.depth = 0
         self.saves: list[tuple[int, int]] = []  # (block, slot)
         self.save_slots: set[int] = set()
-        self.reuse: list[int] = []  # blocks whose before_block_reuse waits come after the saves
+        self.reuse: list[int] = []  # blocks whose before_block_reuse waits come after the copies
         self.restores: list[tuple[int, int, bool]] = []  # (slot, block, wait)
         self.restore_blocks: set[int] = set()
         self.restore_slots: set[int] = set()
@@ -251,10 +264,10 @@ class _CopyBatcher:
         self.restore_blocks, self.restore_slots = set(), set()
         try:
             compute = self._compute()
+            destinations = {block for _, block, _ in restores}
             if saves:
+                saves.sort(key=lambda save: save[0] not in destinations)  # stable: restore targets first
                 self.engine.save([block for block, _ in saves], [slot for _, slot in saves], compute)
-            for block_id in reuse:
-                self.engine.before_block_reuse(block_id, compute)
             start = 0
             while start < len(restores):
                 end, wait = start, restores[start][2]
@@ -263,6 +276,9 @@ class _CopyBatcher:
                 run = restores[start:end]
                 self.engine.restore([slot for slot, _, _ in run], [block for _, block, _ in run], wait, compute)
                 start = end
+            for block_id in reuse:
+                if block_id not in destinations:
+                    self.engine.before_block_reuse(block_id, compute)
         except BaseException:
             if self._on_failure is not None and (saves or restores):
                 self._on_failure(saves, restores)

@@ -3,10 +3,11 @@
 The GPU tests show that batched copies land in order on the device; these pin
 which engine calls the batcher makes and when: outside coalesce() every call
 goes straight through, inside it saves, before_block_reuse waits and restores
-are held back and flushed as saves -> reuse waits -> restores (one call per
-run of equal wait flags), and a copy that must follow a held-back one flushes
-first. A batcher that reordered the flush (restores before saves, or reuse
-waits before the saves they wait on) fails here.
+are held back and flushed as saves (restore targets first) -> restores (one
+call per run of equal wait flags) -> reuse waits (none for blocks restored
+into), and a copy that must follow a held-back one flushes first. A batcher
+that reordered the flush (restores before saves, reuse waits before the
+restores they would hold back) fails here.
 """
 
 import pytest
@@ -51,7 +52,7 @@ def test_calls_go_straight_through_outside_coalesce():
     assert engine.calls == [("save", [3], [0]), ("reuse", 3), ("restore", [0], [5], True), ("use", 5)]
 
 
-def test_flush_order_is_saves_then_reuse_waits_then_restore_runs():
+def test_flush_order_is_saves_then_restore_runs_then_reuse_waits():
     engine, batcher = make()
     with batcher.coalesce():
         batcher.restore(10, 1, True)
@@ -65,13 +66,29 @@ def test_flush_order_is_saves_then_reuse_waits_then_restore_runs():
         assert engine.calls == []
     assert engine.calls == [
         ("save", [2, 5], [20, 21]),
-        ("reuse", 2),
-        ("reuse", 5),
         ("restore", [10, 11], [1, 3], True),
         ("restore", [12], [4], False),
         ("restore", [13], [6], True),
+        ("reuse", 2),
+        ("reuse", 5),
     ]
     assert not (batcher.saves or batcher.reuse or batcher.restores)
+
+
+def test_recycled_victims_restored_into_are_saved_first_and_get_no_reuse_wait():
+    # The block manager's admission: each victim is saved and ordered for reuse, then some are restored into.
+    engine, batcher = make()
+    with batcher.coalesce():
+        for block, slot in ((3, 20), (7, 21), (9, 22)):
+            batcher.save(block, slot)
+            batcher.before_block_reuse(block)
+        batcher.restore(30, 9, False)
+        batcher.restore(31, 7, False)
+    assert engine.calls == [
+        ("save", [7, 9, 3], [21, 22, 20]),
+        ("restore", [30, 31], [9, 7], False),
+        ("reuse", 3),
+    ]
 
 
 def test_reuse_wait_without_held_back_saves_is_immediate():
