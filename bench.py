@@ -845,6 +845,24 @@ def host_link_leg(torch, pool, layout, sources, dests, reps, fmt=None, ceilings=
         # One block per call (the reference's BlockManager), and four (a small batch, as kvx's BlockManager
         # issues from its admission and release loops).
         per_block, per_4_blocks = calls_of(1), calls_of(4)
+
+        # An admission under memory pressure (block_manager.py:97-116, 290-302): the victims are saved, then
+        # CPU entries are restored into those same blocks, waited for. Each restore chunk waits only for the
+        # save kernel that read its destinations, so the restores' copies overlap the saves' transfers.
+        victims_saved = timed(lambda: engine.save(sources, high, compute), "host link: recycle, saves alone")
+        restored_alone = timed(lambda: engine.restore(low, sources, True, compute),
+                               "host link: recycle, restores alone")
+
+        def recycle():
+            engine.save(sources, high, compute)
+            engine.restore(low, sources, True, compute)
+
+        recycled = timed(recycle, "host link: recycle, save victims then restore into them")
+        recycle = {"staging_entries": max(1, min(_MAX_BATCH, _STAGING_BYTES // stride)),
+                   "save_s": round(victims_saved, 5), "restore_s": round(restored_alone, 5),
+                   "both_s": round(recycled, 5), "duplex_gbs": round(gbs(2 * link_bytes, recycled), 2),
+                   "overlap_fraction": round((victims_saved + restored_alone - recycled)
+                                             / min(victims_saved, restored_alone), 3)}
         engine.set_staging(save_staging, restore_staging, n)
 
         ceil_d2h = ceil_h2d = ceil_both = None
@@ -892,6 +910,7 @@ def host_link_leg(torch, pool, layout, sources, dests, reps, fmt=None, ceilings=
             "peak_per_direction_gbs": PCIE_PEAK_GBS,
             "frac_duplex_of_spec": round(duplex / (2 * PCIE_PEAK_GBS), 3),
             "pin_seconds": round(pin_s, 2),
+            "recycle": recycle,
             "logical_kv_gbs": round(2 * n * BF16_BLOCK_BYTES / both_s / 1e9, 2),
             "streams_concurrent": engine.streams_concurrent,
             "per_block_calls": per_block,
