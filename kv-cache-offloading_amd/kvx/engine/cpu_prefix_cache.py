@@ -32,8 +32,8 @@ from kvx.engine.block_manager import BlockManager
 # call covers many entries (cpu_prefix_cache.py:11-13).
 _SLAB_CHUNK_BYTES = 1 << 30
 
-# Device staging per copy stream: entries of one save/restore batch (52
-# Qwen3-8B FP8 entries). A batch larger than the staging is processed in
+# Device staging per copy stream: entries of one save/restore batch (55
+# Qwen3-8B FP8 entries with fp32 scales). A batch larger than the staging is processed in
 # chunks, and on one stream each chunk's kernel waits for the previous
 # chunk's transfer; a larger staging reads more of a batch's blocks at once.
 _STAGING_BYTES = 1 << 30
