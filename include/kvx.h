@@ -241,8 +241,11 @@ int kvx_cache_save_noalloc(kvx_cache* cache, const int32_t* block_ids_host, cons
  * appear only once per call (KVX_E_INVALID). Calls of one or two blocks with
  * wait != 0, issued while no save is in flight, have the restore kernel read
  * the slots itself (a capped grid, system-scope loads), queued on
- * compute_stream, which waits for them anyway; others are staged in device
- * memory by an H2D copy first, on the restore stream.
+ * compute_stream, which waits for them anyway; such a restore also waits
+ * for a pending restore (wait == 0) still writing one of its blocks, which
+ * the restore stream's order gives the others (a prefetched block recycled
+ * before its first use). Others are staged in device memory by an H2D copy
+ * first, on the restore stream.
  */
 int kvx_cache_restore(kvx_cache* cache, const int32_t* slots_host, const int32_t* block_ids_host,
                       int32_t n, int32_t wait, void* compute_stream);
@@ -265,12 +268,15 @@ int kvx_cache_counters(kvx_cache* cache, int64_t* saved_blocks, int64_t* restore
  *   KVX_DEBUG_SKIP_SLOT_READ_WAIT  a save does not wait for restores reading its slot
  *   KVX_DEBUG_SKIP_REUSE_WAIT      before_block_reuse does not wait for the block's save
  *   KVX_DEBUG_SKIP_VICTIM_WAIT     a restore does not wait for a pending save of its destination
+ *   KVX_DEBUG_SKIP_OVERWRITE_WAIT  a restore on compute_stream does not wait for a pending restore
+ *                                  of its destination
  * Results are wrong (never a fault) while a flag is set; 0 restores normal operation.
  */
 #define KVX_DEBUG_SKIP_SAVE_WAIT 1
 #define KVX_DEBUG_SKIP_SLOT_READ_WAIT 2
 #define KVX_DEBUG_SKIP_REUSE_WAIT 4
 #define KVX_DEBUG_SKIP_VICTIM_WAIT 8
+#define KVX_DEBUG_SKIP_OVERWRITE_WAIT 16
 int kvx_cache_set_debug(kvx_cache* cache, int32_t flags);
 
 /*

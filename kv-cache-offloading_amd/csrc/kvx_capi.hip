@@ -1004,6 +1004,19 @@ int kvx_cache_restore(kvx_cache* c, const int32_t* slots, const int32_t* ids, in
     }
     return KVX_OK;
   };
+  // A restore on the caller's stream is not behind the restore stream's
+  // queue: it also waits for a background restore (a prefetch) still writing
+  // one of its blocks, as when a prefetched block is recycled before its
+  // first use without before_block_reuse (block_manager.py:168).
+  auto wait_overwrites = [&]() -> int {
+    if (s == c->restore_stream || (c->debug & KVX_DEBUG_SKIP_OVERWRITE_WAIT)) return KVX_OK;
+    for (int32_t i = 0; i < n; ++i)
+      if (Event* pr = c->pending_restore[ids[i]]) {
+        const int r = c->wait_event(s, pr);
+        if (r) return r;
+      }
+    return KVX_OK;
+  };
   // Before the first kernel: the destinations may still be read by kernels
   // queued on the caller's stream (:375-379). The copies into staging before
   // it touch no destination, so they start without these waits, beside the
@@ -1012,6 +1025,7 @@ int kvx_cache_restore(kvx_cache* c, const int32_t* slots, const int32_t* ids, in
     rc = c->wait_stream(s, compute);
     if (!rc) rc = wait_slots(0, n);
     if (!rc) rc = wait_victims(0, n);
+    if (!rc) rc = wait_overwrites();
     if (!rc) rc = c->launch(false, ids, nullptr, slots, n, s);
     if (rc) return rc;
   } else {
@@ -1079,7 +1093,7 @@ int kvx_cache_before_block_use(kvx_cache* c, int32_t block_id, void* compute_str
 int kvx_cache_set_debug(kvx_cache* c, int32_t flags) {
   if (!c) return set_error(KVX_E_INVALID, "NULL cache");
   if (flags & ~(KVX_DEBUG_SKIP_SAVE_WAIT | KVX_DEBUG_SKIP_SLOT_READ_WAIT | KVX_DEBUG_SKIP_REUSE_WAIT |
-                KVX_DEBUG_SKIP_VICTIM_WAIT))
+                KVX_DEBUG_SKIP_VICTIM_WAIT | KVX_DEBUG_SKIP_OVERWRITE_WAIT))
     return set_error(KVX_E_INVALID, "unknown debug flags %d", flags);
   c->debug = flags;
   return KVX_OK;

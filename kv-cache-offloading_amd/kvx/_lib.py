@@ -20,6 +20,7 @@ E_INVALID, E_RANGE, E_STATE, E_UNSUPPORTED = -1, -2, -3, -4
 SCALE_BF16, SCALE_FP32 = 0, 1
 FORMAT_RAW, FORMAT_FP8 = 0, 1
 DEBUG_SKIP_SAVE_WAIT, DEBUG_SKIP_SLOT_READ_WAIT, DEBUG_SKIP_REUSE_WAIT, DEBUG_SKIP_VICTIM_WAIT = 1, 2, 4, 8
+DEBUG_SKIP_OVERWRITE_WAIT = 16
 NOALLOC_SCRATCH_BYTES = 64 << 20  # KVX_NOALLOC_SCRATCH_BYTES
 
 _c_p = ctypes.c_void_p

@@ -1,0 +1,254 @@
+"""A CPU model of libkvx's copy engine over in-order streams, for ordering tests.
+
+Streams run their queued operations in order. A wait holds its stream until
+its event has completed, and an event completes when its stream reaches it.
+Which runnable stream goes next is picked by a seeded random scheduler, which
+also decides how much device work runs between two host calls. One run is thus
+one of the interleavings the hardware allows for the waits the engine queued.
+Kernels and DMA pieces are atomic operations on block, slot and staging values.
+
+`ModelEngine` has `_CopyEngine`'s interface and queues the work and waits that
+kvx_cache queues (kv-cache-offloading_amd/csrc/kvx_capi.hip):
+- save_blocks_to_slots:
+  - the save stream waits for a busy caller stream;
+  - with split streams, it also waits for each slot's last restore read and for
+    each block's pending restore;
+  - a kernel-written save for 1-2 blocks behind a busy caller stream, else
+    staged chunks (kernel, "block read" event, DMA);
+  - "slot written" after the copies;
+- kvx_cache_restore:
+  - a kernel-read restore on the caller's stream for 1-2 waited blocks with no
+    save in flight, else staged chunks;
+  - each chunk's copy waits for its slots' saves, and its kernel waits for its
+    victims' save kernels;
+  - the first kernel waits for the caller's stream;
+  - a restore on the caller's stream also waits for pending restores into its blocks;
+- kvx_cache_before_block_reuse / _use;
+- events that have already completed are not waited for (hipEventQuery).
+`debug` drops the rules kvx_cache_set_debug drops.
+"""
+
+import random
+from collections import deque
+
+SKIP_SAVE_WAIT, SKIP_SLOT_READ_WAIT, SKIP_REUSE_WAIT, SKIP_VICTIM_WAIT, SKIP_OVERWRITE_WAIT = 1, 2, 4, 8, 16  # KVX_DEBUG_*
+MAX_BATCH = 128  # kMaxBatch
+COMPUTE = "compute"
+
+
+class Event:
+    __slots__ = ("done",)
+
+    def __init__(self):
+        self.done = False
+
+
+class Device:
+    """Streams of queued operations, run by a seeded random scheduler."""
+
+    def __init__(self, rng: random.Random, streams):
+        self.rng = rng
+        self.queues = {name: deque() for name in streams}
+
+    def idle(self, stream) -> bool:
+        """hipStreamQuery: nothing queued on `stream` is left to run."""
+        return not self.queues[stream]
+
+    def record(self, stream) -> Event:
+        event = Event()
+        self.queues[stream].append(("record", event))
+        return event
+
+    def wait(self, stream, event: Event):
+        self.queues[stream].append(("wait", event))
+
+    def run(self, stream, op):
+        self.queues[stream].append(("run", op))
+
+    def step(self) -> bool:
+        ready = [s for s, q in self.queues.items() if q and (q[0][0] != "wait" or q[0][1].done)]
+        if not ready:
+            return False
+        kind, arg = self.queues[self.rng.choice(ready)].popleft()
+        if kind == "record":
+            arg.done = True
+        elif kind == "run":
+            arg()
+        return True
+
+    def advance(self, most: int):
+        """Lets up to `most` device operations run, as between two host calls."""
+        for _ in range(self.rng.randrange(most + 1)):
+            if not self.step():
+                return
+
+    def drain(self):
+        while self.step():
+            pass
+        stuck = {s: len(q) for s, q in self.queues.items() if q}
+        if stuck:
+            raise RuntimeError(f"streams wait forever: {stuck}")
+
+
+class Memory:
+    """Values of the pool's blocks and of the host slots (None: never written)."""
+
+    def __init__(self, num_blocks: int, num_slots: int):
+        self.blocks = [("initial", b) for b in range(num_blocks)]
+        self.slots = [None] * num_slots
+
+
+class ModelEngine:
+    """kvx_cache's ordering rules over a Device and a Memory."""
+
+    def __init__(self, device: Device, memory: Memory, split: bool, staging_entries: int,
+                 kernel_reads: bool = True, debug: int = 0):
+        self.dev, self.mem = device, memory
+        self.split = split
+        self.save_stream = "save"
+        self.restore_stream = "restore" if split else "save"
+        self.staging_entries = staging_entries
+        save_staging = [None] * staging_entries
+        self.staging = {"save": save_staging,
+                        "restore": [None] * staging_entries if split else save_staging}
+        self.host_reads_ok = kernel_reads
+        self.debug = debug
+        nb, ns = len(memory.blocks), len(memory.slots)
+        self.pending_save, self.pending_restore = [None] * nb, [None] * nb
+        self.slot_saved, self.slot_read = [None] * ns, [None] * ns
+        self.last_save = None
+        self.calls = []  # (kind, path) for coverage checks
+
+    # -- waits ------------------------------------------------------------------------------
+
+    def _wait_event(self, stream, event):
+        if event is not None and not event.done:
+            self.dev.wait(stream, event)
+
+    def _wait_stream(self, dst, src) -> bool:
+        busy = dst != src and not self.dev.idle(src)
+        if busy:
+            self.dev.wait(dst, self.dev.record(src))
+        return busy
+
+    # -- work -----------------------------------------------------------------------------------
+
+    def _kernel(self, stream, sources, dests):
+        """One launch: dests[i] <- sources[i], where each side is (space, index) in memory or staging."""
+        spaces = {"blocks": self.mem.blocks, "slots": self.mem.slots, **self.staging}
+
+        def space(name):
+            return spaces[name]
+
+        def op():
+            values = [space(s)[i] for s, i in sources]
+            for (d, i), v in zip(dests, values):
+                space(d)[i] = v
+
+        self.dev.run(stream, op)
+
+    @staticmethod
+    def _distinct(values, what):
+        if len(set(values)) != len(values):
+            raise ValueError(f"a {what} named twice in one call")  # KVX_E_INVALID
+
+    def save(self, block_ids, slots, compute):
+        block_ids, slots = list(block_ids), list(slots)
+        self._distinct(slots, "slot")
+        if not block_ids:
+            return
+        s = self.save_stream
+        busy = self._wait_stream(s, compute)
+        if self.split and not self.debug & SKIP_SLOT_READ_WAIT:
+            for slot in slots:
+                if self.slot_read[slot] is not None:
+                    self._wait_event(s, self.slot_read[slot])
+                    self.slot_read[slot] = None
+        if self.split:
+            for b in block_ids:
+                self._wait_event(s, self.pending_restore[b])
+        direct = len(block_ids) <= 2 and busy
+        self.calls.append(("save", "direct" if direct else "staged"))
+        if direct:
+            self._kernel(s, [("blocks", b) for b in block_ids], [("slots", t) for t in slots])
+        else:
+            step = min(self.staging_entries, MAX_BATCH)
+            for base in range(0, len(block_ids), step):
+                ids, to = block_ids[base:base + step], slots[base:base + step]
+                self._kernel(s, [("blocks", b) for b in ids], [("save", i) for i in range(len(ids))])
+                read = self.dev.record(s)
+                for b in ids:
+                    self.pending_save[b] = read
+                self._kernel(s, [("save", i) for i in range(len(ids))], [("slots", t) for t in to])
+        done = self.dev.record(s)
+        for b, slot in zip(block_ids, slots):
+            if direct:
+                self.pending_save[b] = done
+            self.slot_saved[slot] = done
+        self.last_save = done
+
+    def restore(self, slots, block_ids, wait, compute):
+        slots, block_ids = list(slots), list(block_ids)
+        self._distinct(block_ids, "block")
+        if not block_ids:
+            return
+        n = len(block_ids)
+        direct = (n <= 2 and wait and self.host_reads_ok
+                  and (self.last_save is None or self.last_save.done))
+        s = compute if direct else self.restore_stream
+        order_saves = self.split or s != self.save_stream
+        self.calls.append(("restore", "direct" if direct else "staged"))
+
+        def wait_slots(lo, hi):
+            if order_saves and not self.debug & SKIP_SAVE_WAIT:
+                for slot in slots[lo:hi]:
+                    self._wait_event(s, self.slot_saved[slot])
+
+        def wait_victims(lo, hi):
+            if order_saves and not self.debug & SKIP_VICTIM_WAIT:
+                for slot, b in zip(slots[lo:hi], block_ids[lo:hi]):
+                    ps = self.pending_save[b]
+                    if ps is not None and ps is not self.slot_saved[slot]:
+                        self._wait_event(s, ps)
+
+        if direct:
+            self._wait_stream(s, compute)
+            wait_slots(0, n)
+            wait_victims(0, n)
+            if s != self.restore_stream and not self.debug & SKIP_OVERWRITE_WAIT:
+                for b in block_ids:
+                    self._wait_event(s, self.pending_restore[b])
+            self._kernel(s, [("slots", t) for t in slots], [("blocks", b) for b in block_ids])
+        else:
+            step = min(self.staging_entries, MAX_BATCH)
+            for base in range(0, n, step):
+                hi = min(n, base + step)
+                wait_slots(base, hi)
+                self._kernel(s, [("slots", t) for t in slots[base:hi]], [("restore", i) for i in range(hi - base)])
+                if base == 0:
+                    self._wait_stream(s, compute)
+                wait_victims(base, hi)
+                self._kernel(s, [("restore", i) for i in range(hi - base)], [("blocks", b) for b in block_ids[base:hi]])
+        done = self.dev.record(s)
+        if wait and s != compute:
+            self.dev.wait(compute, done)
+        for slot, b in zip(slots, block_ids):
+            self.slot_read[slot] = done
+            if not wait:
+                self.pending_restore[b] = done
+
+    def before_block_reuse(self, block_id, compute):
+        if self.pending_save[block_id] is not None and self.debug & SKIP_REUSE_WAIT:
+            self.pending_save[block_id] = None
+        for pending in (self.pending_save, self.pending_restore):
+            if pending[block_id] is not None:
+                self._wait_event(compute, pending[block_id])
+                pending[block_id] = None
+
+    def before_block_use(self, block_id, compute):
+        if self.pending_restore[block_id] is not None:
+            self._wait_event(compute, self.pending_restore[block_id])
+            self.pending_restore[block_id] = None
+
+    def synchronize(self):
+        self.dev.drain()

@@ -595,6 +595,47 @@ def test_restores_into_victims_of_a_chunked_save_wait_for_each_chunk_kernel(gpu)
     assert chunked_recycle(gpu)
 
 
+def waited_restore_over_prefetch(gpu, debug: int = 0) -> bool:
+    """A prefetched block recycled before its first use; True if the later, waited restore lands last.
+
+    restore_cached_block reserves its destination without write ordering
+    (block_manager.py:168), so a waited restore can target a block whose
+    prefetch (wait=False, restore stream) is still delayed. The waited restore
+    of one block, with no save in flight, is read by the kernel from the host
+    slot on the caller's stream: it must wait for the prefetch, or the
+    prefetch overwrites it. `debug` drops ordering rules for the negative control.
+    """
+    from kvx.engine.cpu_prefix_cache import _CopyEngine
+
+    g = torch.Generator(device=gpu).manual_seed(41)
+    pool = torch.randn((2, 2, 4, BS, 8, 128), generator=g, device=gpu).to(torch.bfloat16)
+    layout = ops.pool_layout(pool)
+    engine = _CopyEngine(pool, layout, ops.FORMAT_RAW, split=True)
+    try:
+        stride = engine.entry_stride
+        slab = torch.empty(2 * stride, dtype=torch.uint8, pin_memory=True)
+        staging = [torch.empty(2 * stride, dtype=torch.uint8, device=gpu) for _ in range(2)]
+        engine.add_slab(slab, 2)
+        engine.set_staging(*staging, 2)
+        compute = torch.cuda.current_stream(gpu).cuda_stream
+        engine.save([0, 1], [0, 1], compute)
+        engine.synchronize()
+        expected = bf16_bits(pool[:, :, 1])
+        engine.set_debug(debug)
+        ops.sleep(DELAY_US, stream=engine.restore_stream, device=gpu)
+        engine.restore([0], [2], False, compute)  # the prefetch, held up on the restore stream
+        engine.restore([1], [2], True, compute)   # the waited restore into the same block
+        engine.synchronize()
+        torch.cuda.synchronize()
+        return np.array_equal(bf16_bits(pool[:, :, 2]), expected)
+    finally:
+        engine.close()
+
+
+def test_a_waited_restore_into_a_block_still_being_prefetched_lands_last(gpu):
+    assert waited_restore_over_prefetch(gpu)
+
+
 def test_a_failed_batch_withdraws_the_metadata_it_published(gpu, monkeypatch):
     pool = make_pool(gpu, 6)
     manager = BlockManager(6, BS)

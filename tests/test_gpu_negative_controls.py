@@ -194,3 +194,9 @@ def test_chunked_recycle_overwrites_victims_before_their_save_without_the_victim
     from test_gpu_cache import chunked_recycle
 
     assert shows_race(lambda device: not chunked_recycle(device, _lib.DEBUG_SKIP_VICTIM_WAIT), gpu)
+
+
+def test_a_prefetch_overwrites_a_later_waited_restore_without_the_overwrite_wait(gpu):
+    from test_gpu_cache import waited_restore_over_prefetch
+
+    assert shows_race(lambda device: not waited_restore_over_prefetch(device, _lib.DEBUG_SKIP_OVERWRITE_WAIT), gpu)
