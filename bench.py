@@ -655,15 +655,16 @@ def reference_link_leg(torch, pool, sources, dests, scale_dtype, reps=3):
 def handoff_leg(torch, pool, reps=3):
     """KV handoff of one 32,767-token request (128 blocks) on the Qwen3-8B pool: export and import, BF16 and FP8.
 
-    kvx: export_kv's copy (the token gather writes the pinned host payload,
-    quantising it for FP8) and import_kv's (one host-to-device DMA per tensor,
-    then the token scatter, dequantising for FP8), each waited for. Beside
+    kvx: export_kv's and import_kv's copy (kv_handoff.copy_tokens: a group of
+    (K/V, layer) planes at a time through 256 MiB of device staging, the token
+    gather or scatter, quantising or dequantising for FP8, and one DMA per
+    tensor and group), each waited for. Beside
     them, the reference's BF16 copies for the same request on this GPU
     (kv_handoff.py:46-55: index_select, pack, .cpu(); :112-118: .to(device),
     one copy_ per block). `wire_gbs` counts payload bytes (what crosses the
     link), `logical_kv_gbs` the BF16 bytes of the request's KV.
     """
-    from kvx import ops
+    from kvx.engine.kv_handoff import copy_tokens
     from workloads import block_selection
 
     _, layers, nb, bs, heads, hd = pool.shape
@@ -673,7 +674,6 @@ def handoff_leg(torch, pool, reps=3):
     shape = (2, layers, count, heads, hd)
     logical = 2 * layers * count * heads * hd * pool.element_size()
     device = pool.device
-    stream = torch.cuda.current_stream(device)
 
     def timed(fn):
         best = None
@@ -692,21 +692,16 @@ def handoff_leg(torch, pool, reps=3):
     fp8_bytes = codes.numel() + scales.numel() * scales.element_size()
 
     def kvx_export():
-        ops.gather_tokens(pool, table, count, bf16)
-        stream.synchronize()
+        copy_tokens(True, pool, table, count, bf16)
 
     def kvx_import():
-        ops.scatter_tokens(pool, dest, count, bf16.to(device, non_blocking=True))
-        stream.synchronize()
+        copy_tokens(False, pool, dest, count, bf16)
 
     def kvx_export_fp8():
-        ops.gather_tokens_fp8(pool, table, count, codes, scales)
-        stream.synchronize()
+        copy_tokens(True, pool, table, count, codes, scales)
 
     def kvx_import_fp8():
-        ops.scatter_tokens_fp8(pool, dest, count, codes.to(device, non_blocking=True),
-                               scales.to(device, non_blocking=True))
-        stream.synchronize()
+        copy_tokens(False, pool, dest, count, codes, scales)
 
     ids = torch.tensor(table, dtype=torch.int64, device=device)
     held = {}

@@ -224,10 +224,29 @@ def selftest(device=None) -> dict[str, int]:
 # ---------------------------------------------------------------------------
 # Token-granular copies (KV handoff)
 
-def _token_copy(gather: bool, pool: torch.Tensor, block_table, num_tokens: int, dense: torch.Tensor, stream=None):
+def _plane_range(pool: torch.Tensor, layout: BlockLayout, planes) -> tuple[int, BlockLayout, tuple]:
+    """(pool address, layout, leading dense dims) of the pool's (K/V, layer) planes [first, end).
+
+    Plane p is K/V half p // L, layer p % L; None means all 2L planes, whose
+    dense buffers keep the [2, L, ...] shape. A plane range is the same
+    layout with fewer planes, starting at the first one's address.
+    """
+    if planes is None:
+        return pool.data_ptr(), layout, (2, pool.shape[1])
+    first, end = planes
+    if not 0 <= first < end <= layout.planes:
+        raise ValueError(f"plane range [{first}, {end}) is not within the pool's {layout.planes} planes")
+    sub = BlockLayout(*(getattr(layout, name) for name, _ in BlockLayout._fields_))
+    sub.planes = end - first
+    return pool.data_ptr() + first * layout.plane_stride * layout.elem_bytes, sub, (end - first,)
+
+
+def _token_copy(gather: bool, pool: torch.Tensor, block_table, num_tokens: int, dense: torch.Tensor, stream=None,
+                planes=None):
     if pool.ndim != 6:
         raise ValueError("pool must be [2, layers, blocks, block_size, heads, head_dim]")
-    expected = (2, pool.shape[1], num_tokens, *pool.shape[-2:])
+    address, layout, lead = _plane_range(pool, pool_layout(pool), planes)
+    expected = (*lead, num_tokens, *pool.shape[-2:])
     if tuple(dense.shape) != expected or dense.dtype != pool.dtype or not dense.is_contiguous():
         raise ValueError(f"dense buffer must be a contiguous {pool.dtype} tensor of shape {expected}")
     if dense.device.type == "cuda":
@@ -237,30 +256,37 @@ def _token_copy(gather: bool, pool: torch.Tensor, block_table, num_tokens: int, 
     device = _require_device(pool)
     table = list(block_table)
     fn = lib().kvx_gather_tokens if gather else lib().kvx_scatter_tokens
-    check(fn(pool.data_ptr(), ctypes.byref(pool_layout(pool)), int32_array(table), len(table),
-             num_tokens * pool.shape[4], dense.data_ptr(), _stream(device, stream)),
+    check(fn(address, ctypes.byref(layout), int32_array(table), len(table), num_tokens * pool.shape[4],
+             dense.data_ptr(), _stream(device, stream)),
           "gather_tokens" if gather else "scatter_tokens")
 
 
-def gather_tokens(pool: torch.Tensor, block_table, num_tokens: int, out: torch.Tensor, stream=None):
+def gather_tokens(pool: torch.Tensor, block_table, num_tokens: int, out: torch.Tensor, stream=None, planes=None):
     """out[:, :, t] = pool[:, :, block_table[t // BS], t % BS] for t < num_tokens.
 
     `out` is [2, L, num_tokens, H, hd] (kv_handoff.py:46-55's packed payload),
-    on the pool's device or in pinned host memory.
+    on the pool's device or in pinned host memory. With planes=(first, end),
+    only those (K/V, layer) planes (plane p = K/V p // L, layer p % L) are
+    copied, into an `out` of shape [end - first, num_tokens, H, hd].
     """
-    _token_copy(True, pool, block_table, num_tokens, out, stream)
+    _token_copy(True, pool, block_table, num_tokens, out, stream, planes)
 
 
-def scatter_tokens(pool: torch.Tensor, block_table, num_tokens: int, src: torch.Tensor, stream=None):
-    """pool[:, :, block_table[t // BS], t % BS] = src[:, :, t] for t < num_tokens (kv_handoff.py:112-118)."""
-    _token_copy(False, pool, block_table, num_tokens, src, stream)
+def scatter_tokens(pool: torch.Tensor, block_table, num_tokens: int, src: torch.Tensor, stream=None, planes=None):
+    """pool[:, :, block_table[t // BS], t % BS] = src[:, :, t] for t < num_tokens (kv_handoff.py:112-118).
+
+    planes=(first, end) as for gather_tokens."""
+    _token_copy(False, pool, block_table, num_tokens, src, stream, planes)
 
 
 def _token_fp8(gather: bool, pool: torch.Tensor, block_table, num_tokens: int, payload: torch.Tensor,
-               scale: torch.Tensor, stream=None):
+               scale: torch.Tensor, stream=None, planes=None):
     if pool.ndim != 6 or pool.dtype != torch.bfloat16:
         raise ValueError("pool must be a bfloat16 [2, layers, blocks, block_size, heads, head_dim] tensor")
-    shape = (2, pool.shape[1], num_tokens, *pool.shape[-2:])
+    if scale.dtype not in SCALE_DTYPES:
+        raise ValueError("scale must be a bfloat16 or float32 tensor")
+    address, layout, lead = _plane_range(pool, pool_layout(pool, scale.dtype), planes)
+    shape = (*lead, num_tokens, *pool.shape[-2:])
     if tuple(payload.shape) != shape or payload.dtype != torch.float8_e4m3fn or not payload.is_contiguous():
         raise ValueError(f"payload must be a contiguous float8_e4m3fn tensor of shape {shape}")
     if (tuple(scale.shape) != (*shape[:-1], 1) or scale.dtype not in SCALE_DTYPES
@@ -274,22 +300,25 @@ def _token_fp8(gather: bool, pool: torch.Tensor, block_table, num_tokens: int, p
     device = _require_device(pool)
     table = list(block_table)
     fn = lib().kvx_gather_tokens_fp8 if gather else lib().kvx_scatter_tokens_fp8
-    check(fn(pool.data_ptr(), ctypes.byref(pool_layout(pool, scale.dtype)), int32_array(table), len(table),
-             num_tokens * pool.shape[4], payload.data_ptr(), scale.data_ptr(), _stream(device, stream)),
+    check(fn(address, ctypes.byref(layout), int32_array(table), len(table), num_tokens * pool.shape[4],
+             payload.data_ptr(), scale.data_ptr(), _stream(device, stream)),
           "gather_tokens_fp8" if gather else "scatter_tokens_fp8")
 
 
 def gather_tokens_fp8(pool: torch.Tensor, block_table, num_tokens: int, payload: torch.Tensor, scale: torch.Tensor,
-                      stream=None):
+                      stream=None, planes=None):
     """fp8_quantize of gather_tokens' [2, L, num_tokens, H, hd] payload, without the BF16 intermediate.
 
     payload: float8_e4m3fn [2, L, num_tokens, H, hd]; scale: [2, L, num_tokens, H, 1] in bfloat16 or float32,
-    both on the pool's device or in pinned host memory.
+    both on the pool's device or in pinned host memory. planes=(first, end) as for gather_tokens: payload
+    [end - first, num_tokens, H, hd] and scale [end - first, num_tokens, H, 1].
     """
-    _token_fp8(True, pool, block_table, num_tokens, payload, scale, stream)
+    _token_fp8(True, pool, block_table, num_tokens, payload, scale, stream, planes)
 
 
 def scatter_tokens_fp8(pool: torch.Tensor, block_table, num_tokens: int, payload: torch.Tensor, scale: torch.Tensor,
-                       stream=None):
-    """pool[:, :, block_table[t // BS], t % BS] = fp8_dequantize(payload, scale)[:, :, t] (device tensors)."""
-    _token_fp8(False, pool, block_table, num_tokens, payload, scale, stream)
+                       stream=None, planes=None):
+    """pool[:, :, block_table[t // BS], t % BS] = fp8_dequantize(payload, scale)[:, :, t] (device tensors).
+
+    planes=(first, end) as for gather_tokens_fp8."""
+    _token_fp8(False, pool, block_table, num_tokens, payload, scale, stream, planes)

@@ -88,6 +88,40 @@ def test_fp8_token_gather_is_the_codec_of_the_gathered_tokens(gpu, shape, tokens
     assert np.array_equal(bf16_bits(dest), want)
 
 
+@pytest.mark.parametrize("first,end", [(0, 6), (1, 4), (5, 6)])
+def test_token_copies_of_a_plane_range_are_that_slice_of_the_full_copy(gpu, first, end):
+    shape, tokens = SHAPES[0]  # 6 (K/V, layer) planes, > 128 blocks, ragged last block
+    pool = random_pool(gpu, shape, 11, finite=True)
+    table = table_for(shape, tokens, seed=5)
+    host = bf16_bits(pool)
+    full = oracle.gather_tokens(host, table, tokens).reshape(-1, tokens, *shape[-2:])
+    part = torch.empty((end - first, tokens, *shape[-2:]), dtype=pool.dtype, device=gpu)
+    ops.gather_tokens(pool, table, tokens, part, planes=(first, end))
+    assert np.array_equal(bf16_bits(part), full[first:end])
+    payload = torch.empty(part.shape, dtype=torch.float8_e4m3fn, device=gpu)
+    scale = torch.empty((*part.shape[:-1], 1), dtype=torch.float32, device=gpu)
+    ops.gather_tokens_fp8(pool, table, tokens, payload, scale, planes=(first, end))
+    codes, scales = oracle.quantize(full[first:end], True)
+    assert np.array_equal(payload.cpu().view(torch.uint8).numpy(), codes)
+    assert np.array_equal(scale.cpu().view(torch.int32).numpy(), scales.view(np.int32))
+    # Scatters of the range write exactly those planes' token rows.
+    want = np.zeros(shape, dtype=np.uint16)
+    planes = want.reshape(-1, *shape[2:])
+    for p in range(first, end):
+        view = planes[p:p + 1].reshape(1, 1, *shape[2:])
+        oracle.scatter_tokens(view, table, full[p:p + 1].reshape(1, 1, tokens, *shape[-2:]))
+    dest = torch.zeros_like(pool)
+    ops.scatter_tokens(dest, table, tokens, part, planes=(first, end))
+    assert np.array_equal(bf16_bits(dest), want)
+    dest.zero_()
+    ops.scatter_tokens_fp8(dest, table, tokens, payload, scale, planes=(first, end))
+    for p in range(first, end):
+        view = planes[p:p + 1].reshape(1, 1, *shape[2:])
+        back = oracle.dequantize(codes[p - first:p - first + 1], scales[p - first:p - first + 1], True)
+        oracle.scatter_tokens(view, table, back.reshape(1, 1, tokens, *shape[-2:]))
+    assert np.array_equal(bf16_bits(dest), want)
+
+
 def test_token_copies_reject_short_tables_and_bad_buffers(gpu):
     pool = torch.zeros((2, 2, 4, 256, 1, 4), dtype=torch.bfloat16, device=gpu)
     out = torch.empty((2, 2, 300, 1, 4), dtype=pool.dtype, device=gpu)
@@ -158,6 +192,38 @@ def test_detach_then_resume_carries_the_kv_and_decode_continues(gpu, length, fmt
     assert final.outputs == [(destination_id, [10, 11, 12])]
     assert all(not prefill for prefill, _ in destination.model_runner.calls)
     assert not manager.used_block_ids
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("group", [1, 3])
+def test_handoff_in_plane_groups_carries_the_kv(gpu, fmt, group, monkeypatch):
+    """Export and import move the payload through staging a group of planes at a time.
+
+    The staging is shrunk to `group` planes of this 700-token request, so the pool's 4 planes go in groups of
+    1 or of 3 and 1."""
+    source, source_id = running_request(gpu, length=700, budget=1024)
+    pool = source.model_runner.kv_cache
+    row = pool.shape[-1] * (2 if not fmt else 1) + (0 if not fmt else fmt.get("scale_dtype", torch.float32).itemsize)
+    monkeypatch.setattr(kv_handoff, "_STAGING_BYTES", group * 700 * pool.shape[-2] * row)
+    assert len(kv_handoff._plane_groups(pool, 700, torch.bfloat16 if not fmt else torch.float8_e4m3fn,
+                                        fmt.get("scale_dtype", torch.float32) if fmt else None)) == -(-4 // group)
+    table = source.scheduler.running[0].block_table.copy()
+    tokens = oracle.gather_tokens(bf16_bits(pool), table, 700)
+    snapshot = source.detach_request(source_id, **fmt)
+    if fmt:
+        fp32 = fmt.get("scale_dtype", torch.float32) == torch.float32
+        codes, scales = oracle.quantize(tokens, fp32)
+        assert np.array_equal(snapshot.kv.view(torch.uint8).numpy(), codes)
+        assert np.array_equal(snapshot.scale.view(torch.uint8).numpy(), scales.view(np.uint8))
+        tokens = oracle.dequantize(codes, scales, fp32)
+    else:
+        assert np.array_equal(snapshot.kv.view(torch.int16).numpy().view(np.uint16), tokens)
+    destination = cached_engine(gpu, [[11]], budget=1024)
+    destination.model_runner.kv_cache.fill_(-1)
+    destination.resume_request(snapshot)
+    seq = destination.scheduler.running[0]
+    assert np.array_equal(oracle.gather_tokens(bf16_bits(destination.model_runner.kv_cache), seq.block_table, 700),
+                          tokens)
 
 
 @pytest.mark.parametrize("fmt", FORMATS)
