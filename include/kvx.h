@@ -136,7 +136,9 @@ int kvx_restore_blocks(void* pool, const kvx_block_layout* layout, int32_t forma
  * kvx_gather_tokens replaces export_kv's index_select + contiguous
  * (:46-55); kvx_scatter_tokens replaces import_kv's per-block copy_
  * (:112-118). The buffer may be device memory or mapped pinned host memory.
- * A scatter's table may not name a block twice (KVX_E_INVALID).
+ * A scatter's table may not name a block twice (KVX_E_INVALID). To copy only
+ * planes [first, end), pass pool + first * plane_stride * elem_bytes and a
+ * layout with planes = end - first; the buffer then holds those planes.
  */
 int kvx_gather_tokens(const void* pool, const kvx_block_layout* layout, const int32_t* block_table_host,
                       int32_t table_len, int64_t num_rows, void* dst, void* stream);
