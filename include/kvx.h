@@ -184,7 +184,9 @@ int kvx_cache_destroy(kvx_cache* cache);
 /*
  * Attaches one device staging area per stream, each holding `entries`
  * entries of kvx_entry_layout's entry_stride (per-stream staging, :217-223).
- * Pass the same pointer twice when split_streams == 0.
+ * Pass the same pointer twice when split_streams == 0; with split streams the
+ * two areas may not overlap (KVX_E_INVALID). Copies already queued keep
+ * using the previous areas, which must stay allocated until they complete.
  */
 int kvx_cache_set_staging(kvx_cache* cache, void* save_staging, void* restore_staging,
                           int32_t entries);

@@ -894,6 +894,11 @@ int kvx_cache_set_staging(kvx_cache* c, void* save_staging, void* restore_stagin
   int64_t staging_bytes;
   if (!span_product({entries, c->entry_stride}, &staging_bytes))
     return set_error(KVX_E_UNSUPPORTED, "staging of %d entries spans more than 2^40 bytes", entries);
+  // With split streams a save's chunks and a restore's chunks use their
+  // buffers at the same time.
+  const uintptr_t save_at = (uintptr_t)save_staging, restore_at = (uintptr_t)restore_staging;
+  if (c->split && save_at < restore_at + (uintptr_t)staging_bytes && restore_at < save_at + (uintptr_t)staging_bytes)
+    return set_error(KVX_E_INVALID, "split streams need save and restore staging buffers that do not overlap");
   c->save_staging = (uint8_t*)save_staging;
   c->restore_staging = (uint8_t*)restore_staging;
   c->staging_entries = entries;

@@ -636,6 +636,23 @@ def test_a_waited_restore_into_a_block_still_being_prefetched_lands_last(gpu):
     assert waited_restore_over_prefetch(gpu)
 
 
+def test_split_streams_refuse_overlapping_staging(gpu):
+    from kvx.engine.cpu_prefix_cache import _CopyEngine
+
+    pool = torch.zeros((2, 2, 4, BS, 8, 128), dtype=torch.bfloat16, device=gpu)
+    layout = ops.pool_layout(pool, torch.float32)
+    engine = _CopyEngine(pool, layout, ops.FORMAT_FP8, split=True)
+    try:
+        stride = engine.entry_stride
+        buffer = torch.empty(3 * stride, dtype=torch.uint8, device=gpu)
+        for save, restore in ((buffer, buffer), (buffer[:2 * stride], buffer[stride:])):
+            with pytest.raises(ValueError, match="do not overlap"):
+                engine.set_staging(save, restore, 2)
+        engine.set_staging(buffer[:stride], buffer[stride:2 * stride], 1)  # adjacent is fine
+    finally:
+        engine.close()
+
+
 def test_a_failed_batch_withdraws_the_metadata_it_published(gpu, monkeypatch):
     pool = make_pool(gpu, 6)
     manager = BlockManager(6, BS)
