@@ -295,6 +295,7 @@ namespace {
 struct Event {
   hipEvent_t ev = nullptr;
   int refs = 0;
+  hipStream_t stream = nullptr;  // where it was last recorded
 };
 
 struct Slab {
@@ -487,22 +488,29 @@ struct kvx_cache {
     return rc;
   }
 
+  int record(Event* e, hipStream_t s) {
+    e->stream = s;
+    return hip_status(hipEventRecord(e->ev, s), "hipEventRecord");
+  }
+
   // The save kernel just queued on `s` is the last reader of these pool
   // blocks: their pending_save becomes an event recorded now.
   int release_blocks_after(const int32_t* ids, int32_t n, hipStream_t s) {
     Event* read = nullptr;
     int rc = new_event(&read);
-    if (!rc) rc = hip_status(hipEventRecord(read->ev, s), "hipEventRecord");
+    if (!rc) rc = record(read, s);
     if (!rc)
       for (int32_t i = 0; i < n; ++i) assign(pending_save[ids[i]], read);
     if (read) release_if_unused(read);
     return rc;
   }
 
-  // `s` waits for `e`. An event that has already completed orders nothing
-  // queued from now on, so it costs no wait: a one-block restore used to
-  // queue one on its slot's long-finished save.
+  // `s` waits for `e`. An event recorded on `s` itself, or one that has
+  // already completed, orders nothing queued from now on, so it costs no
+  // wait: a one-block restore used to queue one on its slot's long-finished
+  // save.
   int wait_event(hipStream_t s, Event* e) {
+    if (e->stream == s) return KVX_OK;
     const hipError_t q = hipEventQuery(e->ev);
     if (q == hipSuccess) return KVX_OK;
     if (q != hipErrorNotReady) return hip_status(q, "hipEventQuery");
@@ -673,8 +681,11 @@ static int save_blocks_to_slots(kvx_cache* c, const int32_t* ids, const int32_t*
   bool caller_busy = false;
   rc = c->wait_stream(s, compute, &caller_busy);
   if (rc) return rc;
-  // With split streams, after the last restore that read each target slot (:312-314).
-  if (c->split && !(c->debug & KVX_DEBUG_SKIP_SLOT_READ_WAIT)) {
+  // After the last restore that read each target slot (:312-314). With one
+  // copy stream only a kernel-read restore, queued on a caller's stream, is
+  // not already ahead of the save; the wait for `compute` covers it only if
+  // it was queued there.
+  if (!(c->debug & KVX_DEBUG_SKIP_SLOT_READ_WAIT)) {
     for (int32_t i = 0; i < n; ++i) {
       Event*& r = c->slot_read[slots[i]];
       if (r) {
@@ -686,7 +697,7 @@ static int save_blocks_to_slots(kvx_cache* c, const int32_t* ids, const int32_t*
   }
   // After a background restore still writing a source block (a prefetched
   // block whose CPU entry was dropped can be saved again before first use).
-  if (c->split) {
+  {
     for (int32_t i = 0; i < n; ++i) {
       if (Event* pr = c->pending_restore[ids[i]]) {
         rc = c->wait_event(s, pr);
@@ -718,7 +729,7 @@ static int save_blocks_to_slots(kvx_cache* c, const int32_t* ids, const int32_t*
   }
   Event* done = fixed_done;
   if (!done) rc = c->new_event(&done);
-  if (!rc) rc = hip_status(hipEventRecord(done->ev, s), "hipEventRecord");
+  if (!rc) rc = c->record(done, s);
   if (rc) {
     if (done && !fixed_done) c->release_if_unused(done);
     return rc;
@@ -1047,7 +1058,7 @@ int kvx_cache_restore(kvx_cache* c, const int32_t* slots, const int32_t* ids, in
   }
   Event* done = nullptr;
   rc = c->new_event(&done);
-  if (!rc) rc = hip_status(hipEventRecord(done->ev, s), "hipEventRecord");
+  if (!rc) rc = c->record(done, s);
   if (!rc && s == compute) c->track_caller_read(s, done);
   if (!rc && wait && s != compute) rc = c->queue_wait(compute, done);
   if (rc) {

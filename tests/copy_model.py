@@ -11,8 +11,8 @@ Kernels and DMA pieces are atomic operations on block, slot and staging values.
 kvx_cache queues (kv-cache-offloading_amd/csrc/kvx_capi.hip):
 - save_blocks_to_slots:
   - the save stream waits for a busy caller stream;
-  - with split streams, it also waits for each slot's last restore read and for
-    each block's pending restore;
+  - it also waits for each slot's last restore read and for each block's
+    pending restore;
   - a kernel-written save for 1-2 blocks behind a busy caller stream, else
     staged chunks (kernel, "block read" event, DMA);
   - "slot written" after the copies;
@@ -24,7 +24,7 @@ kvx_cache queues (kv-cache-offloading_amd/csrc/kvx_capi.hip):
   - the first kernel waits for the caller's stream;
   - a restore on the caller's stream also waits for pending restores into its blocks;
 - kvx_cache_before_block_reuse / _use;
-- events that have already completed are not waited for (hipEventQuery).
+- events recorded on the waiting stream, or already completed, are not waited for.
 `debug` drops the rules kvx_cache_set_debug drops.
 """
 
@@ -37,10 +37,11 @@ COMPUTE = "compute"
 
 
 class Event:
-    __slots__ = ("done",)
+    __slots__ = ("done", "stream")
 
-    def __init__(self):
+    def __init__(self, stream):
         self.done = False
+        self.stream = stream
 
 
 class Device:
@@ -55,7 +56,7 @@ class Device:
         return not self.queues[stream]
 
     def record(self, stream) -> Event:
-        event = Event()
+        event = Event(stream)
         self.queues[stream].append(("record", event))
         return event
 
@@ -122,7 +123,7 @@ class ModelEngine:
     # -- waits ------------------------------------------------------------------------------
 
     def _wait_event(self, stream, event):
-        if event is not None and not event.done:
+        if event is not None and not event.done and event.stream != stream:
             self.dev.wait(stream, event)
 
     def _wait_stream(self, dst, src) -> bool:
@@ -159,14 +160,13 @@ class ModelEngine:
             return
         s = self.save_stream
         busy = self._wait_stream(s, compute)
-        if self.split and not self.debug & SKIP_SLOT_READ_WAIT:
+        if not self.debug & SKIP_SLOT_READ_WAIT:
             for slot in slots:
                 if self.slot_read[slot] is not None:
                     self._wait_event(s, self.slot_read[slot])
                     self.slot_read[slot] = None
-        if self.split:
-            for b in block_ids:
-                self._wait_event(s, self.pending_restore[b])
+        for b in block_ids:
+            self._wait_event(s, self.pending_restore[b])
         direct = len(block_ids) <= 2 and busy
         self.calls.append(("save", "direct" if direct else "staged"))
         if direct:

@@ -119,6 +119,25 @@ def test_a_waited_restore_into_a_block_still_being_prefetched_lands_last(split):
     assert wrong == 0
 
 
+def test_a_save_waits_for_a_kernel_read_restore_queued_from_another_callers_stream():
+    # One copy stream. A waited one-block restore, read by the kernel from its slot, is queued on caller stream A
+    # behind other work; the slot is then discarded and a save into it issued from caller stream B, which is idle.
+    # The save's wait for B covers nothing A holds, so it must wait for the slot's last read itself.
+    wrong = 0
+    for seed in range(100):
+        dev = Device(random.Random(seed), (COMPUTE, "other", "save"))
+        mem = Memory(4, 2)
+        mem.slots[0] = "entry"
+        engine = ModelEngine(dev, mem, False, 2)
+        dev.run(COMPUTE, lambda: None)  # A is busy
+        engine.restore([0], [1], True, COMPUTE)
+        assert engine.calls[-1] == ("restore", "direct")
+        engine.save([2], [0], "other")
+        dev.drain()
+        wrong += mem.blocks[1] != "entry"
+    assert wrong == 0
+
+
 class RestoresFirst(_CopyBatcher):
     """A wrong flush order: held-back restores before the saves of the victims they overwrite."""
 

@@ -636,6 +636,46 @@ def test_a_waited_restore_into_a_block_still_being_prefetched_lands_last(gpu):
     assert waited_restore_over_prefetch(gpu)
 
 
+def slot_reuse_across_caller_streams(gpu, debug: int = 0) -> bool:
+    """One copy stream; True if a save into a slot waits for a kernel-read restore queued from another stream.
+
+    A waited one-block restore with no save in flight is read by the kernel
+    from its slot on the caller's stream, here a side stream A held up by a
+    delay. The slot is then reused by a save issued from the idle current
+    stream B. The save's wait for B does not cover A, so it must wait for the
+    slot's last read itself. `debug` drops ordering rules for the negative control.
+    """
+    from kvx.engine.cpu_prefix_cache import _CopyEngine
+
+    g = torch.Generator(device=gpu).manual_seed(43)
+    pool = torch.randn((2, 2, 4, BS, 8, 128), generator=g, device=gpu).to(torch.bfloat16)
+    engine = _CopyEngine(pool, ops.pool_layout(pool), ops.FORMAT_RAW, split=False)
+    try:
+        stride = engine.entry_stride
+        slab = torch.empty(2 * stride, dtype=torch.uint8, pin_memory=True)
+        staging = torch.empty(2 * stride, dtype=torch.uint8, device=gpu)
+        engine.add_slab(slab, 2)
+        engine.set_staging(staging, staging, 2)
+        current = torch.cuda.current_stream(gpu)
+        engine.save([0], [0], current.cuda_stream)
+        engine.synchronize()
+        expected = bf16_bits(pool[:, :, 0])
+        engine.set_debug(debug)
+        side = torch.cuda.Stream(gpu)
+        ops.sleep(DELAY_US, stream=side, device=gpu)
+        engine.restore([0], [1], True, side.cuda_stream)  # read by the kernel on the side stream
+        engine.save([2], [0], current.cuda_stream)        # the slot, reused from the idle current stream
+        engine.synchronize()
+        torch.cuda.synchronize()
+        return np.array_equal(bf16_bits(pool[:, :, 1]), expected)
+    finally:
+        engine.close()
+
+
+def test_a_save_waits_for_a_kernel_read_restore_queued_from_another_callers_stream(gpu):
+    assert slot_reuse_across_caller_streams(gpu)
+
+
 def test_split_streams_refuse_overlapping_staging(gpu):
     from kvx.engine.cpu_prefix_cache import _CopyEngine
 

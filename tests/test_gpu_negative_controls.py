@@ -200,3 +200,9 @@ def test_a_prefetch_overwrites_a_later_waited_restore_without_the_overwrite_wait
     from test_gpu_cache import waited_restore_over_prefetch
 
     assert shows_race(lambda device: not waited_restore_over_prefetch(device, _lib.DEBUG_SKIP_OVERWRITE_WAIT), gpu)
+
+
+def test_a_save_overwrites_a_slot_another_callers_stream_still_reads_without_the_slot_read_wait(gpu):
+    from test_gpu_cache import slot_reuse_across_caller_streams
+
+    assert shows_race(lambda device: not slot_reuse_across_caller_streams(device, _lib.DEBUG_SKIP_SLOT_READ_WAIT), gpu)
