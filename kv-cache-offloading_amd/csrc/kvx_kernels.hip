@@ -82,11 +82,12 @@ __device__ __forceinline__ uint32_t load_host32(__amdgpu_buffer_rsrc_t r, int of
 // turn; kChunk < 0 gives each XCD one contiguous eighth of the grid. Measured
 // on the Qwen3-8B block workload: one eighth per XCD (instead of every 8th
 // tile) raised the FP8 kernels from ~5.5 to ~6.2-6.5 TB/s, and no run length
-// beats it for the restore and store_kvcache kernels; the save kernel gains
-// ~1% with runs of 1024 tiles (8 planes), the BF16 copies ~1.5% with runs of
-// 64 tiles (one 512 KiB plane).
+// beats it for the restore and store_kvcache kernels. The save kernel alone
+// gains ~1% with runs of 1024 tiles, but a restore launched after such a save
+// ran 0.4-0.5% slower, so the save keeps one eighth per XCD too. The BF16
+// copies gain ~1.5% with runs of 64 tiles (one 512 KiB plane).
 constexpr int kXcds = 8;
-constexpr int kSaveXcdRun = 1024;
+constexpr int kSaveXcdRun = -1;
 constexpr int kCopyXcdRun = 64;
 template <int kChunk = -1>
 __device__ __forceinline__ int xcd_tile(int bid, int grid) {
