@@ -24,7 +24,10 @@ kvx_cache queues (kv-cache-offloading_amd/csrc/kvx_capi.hip):
   - the first kernel waits for the caller's stream;
   - a restore on the caller's stream also waits for pending restores into its blocks;
 - kvx_cache_before_block_reuse / _use;
-- events recorded on the waiting stream, or already completed, are not waited for.
+- events recorded on the waiting stream, or already completed, are not waited for;
+- kvx_cache_save_noalloc (`save(..., fixed=True)`): the static staging array, no
+  per-chunk "block read" events, and one event the cache re-records for every
+  such save, so a wait on it waits for its latest record (hipEventRecord).
 `debug` drops the rules kvx_cache_set_debug drops.
 """
 
@@ -42,6 +45,17 @@ class Event:
     def __init__(self, stream):
         self.done = False
         self.stream = stream
+
+
+class FixedEvent:
+    """One event re-recorded by every allocation-free save: waiting on it waits for its latest record."""
+
+    def __init__(self):
+        self.current = None
+
+
+def latest(event):
+    return event.current if isinstance(event, FixedEvent) else event
 
 
 class Device:
@@ -103,7 +117,7 @@ class ModelEngine:
     """kvx_cache's ordering rules over a Device and a Memory."""
 
     def __init__(self, device: Device, memory: Memory, split: bool, staging_entries: int,
-                 kernel_reads: bool = True, debug: int = 0):
+                 kernel_reads: bool = True, debug: int = 0, static_entries: int = 4):
         self.dev, self.mem = device, memory
         self.split = split
         self.save_stream = "save"
@@ -111,7 +125,10 @@ class ModelEngine:
         self.staging_entries = staging_entries
         save_staging = [None] * staging_entries
         self.staging = {"save": save_staging,
-                        "restore": [None] * staging_entries if split else save_staging}
+                        "restore": [None] * staging_entries if split else save_staging,
+                        "static": [None] * static_entries}
+        self.static_entries = static_entries
+        self.fixed = FixedEvent()
         self.host_reads_ok = kernel_reads
         self.debug = debug
         nb, ns = len(memory.blocks), len(memory.slots)
@@ -123,6 +140,7 @@ class ModelEngine:
     # -- waits ------------------------------------------------------------------------------
 
     def _wait_event(self, stream, event):
+        event = latest(event)
         if event is not None and not event.done and event.stream != stream:
             self.dev.wait(stream, event)
 
@@ -153,11 +171,13 @@ class ModelEngine:
         if len(set(values)) != len(values):
             raise ValueError(f"a {what} named twice in one call")  # KVX_E_INVALID
 
-    def save(self, block_ids, slots, compute):
+    def save(self, block_ids, slots, compute, fixed: bool = False):
         block_ids, slots = list(block_ids), list(slots)
         self._distinct(slots, "slot")
         if not block_ids:
             return
+        if fixed and len(block_ids) > self.static_entries:
+            raise IndexError("more blocks than the static staging holds")  # KVX_E_RANGE
         s = self.save_stream
         busy = self._wait_stream(s, compute)
         if not self.debug & SKIP_SLOT_READ_WAIT:
@@ -168,21 +188,26 @@ class ModelEngine:
         for b in block_ids:
             self._wait_event(s, self.pending_restore[b])
         direct = len(block_ids) <= 2 and busy
-        self.calls.append(("save", "direct" if direct else "staged"))
+        self.calls.append(("save", "direct" if direct else "staged") + (("fixed",) if fixed else ()))
+        staging = "static" if fixed else "save"
         if direct:
             self._kernel(s, [("blocks", b) for b in block_ids], [("slots", t) for t in slots])
         else:
-            step = min(self.staging_entries, MAX_BATCH)
+            step = min(self.static_entries if fixed else self.staging_entries, MAX_BATCH)
             for base in range(0, len(block_ids), step):
                 ids, to = block_ids[base:base + step], slots[base:base + step]
-                self._kernel(s, [("blocks", b) for b in ids], [("save", i) for i in range(len(ids))])
-                read = self.dev.record(s)
-                for b in ids:
-                    self.pending_save[b] = read
-                self._kernel(s, [("save", i) for i in range(len(ids))], [("slots", t) for t in to])
+                self._kernel(s, [("blocks", b) for b in ids], [(staging, i) for i in range(len(ids))])
+                if not fixed:
+                    read = self.dev.record(s)
+                    for b in ids:
+                        self.pending_save[b] = read
+                self._kernel(s, [(staging, i) for i in range(len(ids))], [("slots", t) for t in to])
         done = self.dev.record(s)
+        if fixed:
+            self.fixed.current = done
+            done = self.fixed
         for b, slot in zip(block_ids, slots):
-            if direct:
+            if direct or fixed:
                 self.pending_save[b] = done
             self.slot_saved[slot] = done
         self.last_save = done
@@ -194,7 +219,7 @@ class ModelEngine:
             return
         n = len(block_ids)
         direct = (n <= 2 and wait and self.host_reads_ok
-                  and (self.last_save is None or self.last_save.done))
+                  and (self.last_save is None or latest(self.last_save).done))
         s = compute if direct else self.restore_stream
         order_saves = self.split or s != self.save_stream
         self.calls.append(("restore", "direct" if direct else "staged"))

@@ -190,6 +190,26 @@ class Caller:
         return bad
 
 
+class NoAllocSaves:
+    """An engine whose saves of up to `fits` blocks go through the allocation-free entry point.
+
+    `save_noalloc(block_ids, slots, compute)` is that entry point; larger saves, and everything else, go to
+    `engine` as usual, so sequences mix both kinds of save.
+    """
+
+    def __init__(self, engine, save_noalloc, fits: int):
+        self.engine, self._save_noalloc, self.fits = engine, save_noalloc, fits
+
+    def save(self, block_ids, slots, compute):
+        if len(block_ids) <= self.fits:
+            self._save_noalloc(block_ids, slots, compute)
+        else:
+            self.engine.save(block_ids, slots, compute)
+
+    def __getattr__(self, name):
+        return getattr(self.engine, name)
+
+
 class _Nothing:
     def __enter__(self):
         return self

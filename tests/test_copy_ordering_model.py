@@ -17,7 +17,7 @@ import pytest
 
 from copy_model import (COMPUTE, SKIP_OVERWRITE_WAIT, SKIP_REUSE_WAIT, SKIP_SAVE_WAIT, SKIP_SLOT_READ_WAIT,
                         SKIP_VICTIM_WAIT, Device, Memory, ModelEngine)
-from copy_scenarios import Caller
+from copy_scenarios import Caller, NoAllocSaves
 from kvx.engine.cpu_prefix_cache import _CopyBatcher
 
 BLOCKS, SLOTS, ROUNDS = 12, 10, 60
@@ -25,11 +25,15 @@ BLOCKS, SLOTS, ROUNDS = 12, 10, 60
 
 class ModelBackend:
     def __init__(self, seed: int, split: bool, staging: int, kernel_reads: bool = True, debug: int = 0,
-                 batcher=_CopyBatcher):
+                 batcher=_CopyBatcher, noalloc: bool = False):
         self.dev = Device(random.Random(seed * 7919 + 1), (COMPUTE, "save", "restore"))
         self.mem = Memory(BLOCKS, SLOTS)
         self.engine = ModelEngine(self.dev, self.mem, split, staging, kernel_reads, debug)
-        self.batcher = batcher(self.engine, lambda: COMPUTE)
+        engine = self.engine
+        if noalloc:
+            engine = NoAllocSaves(self.engine, lambda ids, slots, compute: self.engine.save(ids, slots, compute, True),
+                                  self.engine.static_entries)
+        self.batcher = batcher(engine, lambda: COMPUTE)
 
     def write(self, block, value):
         def op():
@@ -58,8 +62,8 @@ class ModelBackend:
         return self.mem.slots[slot]
 
 
-def run(seed, split, staging, batched=True, kernel_reads=True, debug=0, batcher=_CopyBatcher):
-    backend = ModelBackend(seed, split, staging, kernel_reads, debug, batcher)
+def run(seed, split, staging, batched=True, kernel_reads=True, debug=0, batcher=_CopyBatcher, noalloc=False):
+    backend = ModelBackend(seed, split, staging, kernel_reads, debug, batcher, noalloc)
     caller = Caller(random.Random(seed), backend, BLOCKS, SLOTS, batched=batched)
     caller.run(ROUNDS)
     return caller.check(), caller, backend
@@ -81,6 +85,18 @@ def test_every_interleaving_found_gives_the_sequential_result(split, staging, ba
     # kernel-read restores where they are allowed.
     assert ("save", "staged") in paths and ("restore", "staged") in paths and ("save", "direct") in paths
     assert (("restore", "direct") in paths) == kernel_reads
+
+
+@pytest.mark.parametrize("split,staging,batched", [(True, 1, True), (True, 3, False), (False, 2, True),
+                                                   (False, 1, False)])
+def test_allocation_free_saves_keep_the_sequential_result(split, staging, batched):
+    # Saves of up to 4 blocks go through kvx_cache_save_noalloc's rules (static staging, one re-recorded event).
+    paths = set()
+    for seed in range(40):
+        bad, caller, backend = run(seed, split, staging, batched, noalloc=True)
+        assert not bad, f"seed {seed}: {bad[:5]}\n" + "\n".join(caller.log[-40:])
+        paths.update(backend.engine.calls)
+    assert ("save", "staged", "fixed") in paths and ("save", "direct", "fixed") in paths
 
 
 def fails_somewhere(seeds=60, **kwargs) -> bool:

@@ -8,7 +8,8 @@ restore stream or the caller's stream, so copies lag behind the caller's work, o
 copies. Every read the caller's stream makes, and every block and live entry at the end, must hold what
 a sequential execution gives. The CPU model (test_copy_ordering_model.py) explores the interleavings;
 this runs the same sequences on the hardware, FP8 and BF16 entries, split streams and one copy stream,
-batched and one call per block.
+batched and one call per block, and with saves of up to 4 blocks through the allocation-free entry point
+(kvx_cache_save_noalloc).
 """
 
 import random
@@ -17,8 +18,9 @@ import numpy as np
 import pytest
 import torch
 
-from copy_scenarios import Caller
-from kvx import ops
+from copy_scenarios import Caller, NoAllocSaves
+from kvx import _lib, ops
+from kvx._lib import check, int32_array, lib
 from kvx.engine.cpu_prefix_cache import _CopyBatcher, _CopyEngine
 
 pytestmark = pytest.mark.gpu
@@ -41,7 +43,7 @@ def bf16_bits_of(value: int, fp8: bool) -> int:
 
 
 class GpuBackend:
-    def __init__(self, device, seed: int, fmt: int, split: bool, staging: int):
+    def __init__(self, device, seed: int, fmt: int, split: bool, staging: int, noalloc: bool = False):
         self.device, self.fmt = device, fmt
         self.fp8 = fmt == ops.FORMAT_FP8
         self.rng = random.Random(seed * 104729 + 3)
@@ -56,7 +58,16 @@ class GpuBackend:
         self.staging = (save, restore)
         self.engine.add_slab(self.slab, SLOTS)
         self.engine.set_staging(save, restore, staging)
-        self.batcher = _CopyBatcher(self.engine, lambda: torch.cuda.current_stream(device).cuda_stream)
+        engine = self.engine
+        if noalloc:
+            assert _lib.NOALLOC_SCRATCH_BYTES // self.stride >= 4
+
+            def save_noalloc(block_ids, slots, compute):
+                check(lib().kvx_cache_save_noalloc(self.engine.handle, int32_array(block_ids), int32_array(slots),
+                                                   len(block_ids), compute), "kvx_cache_save_noalloc")
+
+            engine = NoAllocSaves(self.engine, save_noalloc, 4)
+        self.batcher = _CopyBatcher(engine, lambda: torch.cuda.current_stream(device).cuda_stream)
         self.reads = torch.empty((ROUNDS * 8 + 8, *self.pool[:, :, 0].shape), dtype=torch.bfloat16, device=device)
         self.n_reads = 0
         self.decode = {}  # bf16 bits -> value id
@@ -112,11 +123,12 @@ class GpuBackend:
 
 
 @pytest.mark.parametrize("fmt", [ops.FORMAT_FP8, ops.FORMAT_RAW], ids=["fp8", "bf16"])
-@pytest.mark.parametrize("split,staging,batched", [(True, 3, True), (True, 1, False), (False, 2, True),
-                                                   (True, 128, True)])
-def test_random_caller_sequences_give_the_sequential_result(gpu, fmt, split, staging, batched):
+@pytest.mark.parametrize("split,staging,batched,noalloc", [(True, 3, True, False), (True, 1, False, False),
+                                                           (False, 2, True, False), (True, 128, True, False),
+                                                           (True, 3, True, True), (False, 1, False, True)])
+def test_random_caller_sequences_give_the_sequential_result(gpu, fmt, split, staging, batched, noalloc):
     for seed in range(6):
-        backend = GpuBackend(gpu, seed, fmt, split, staging)
+        backend = GpuBackend(gpu, seed, fmt, split, staging, noalloc)
         try:
             caller = Caller(random.Random(seed), backend, BLOCKS, SLOTS, batched=batched)
             caller.run(ROUNDS)
