@@ -445,9 +445,9 @@ def save_on_release_while_blocked(api):
 # ---------------------------------------------------------------------------
 # Scheduler scenarios: schedule() / postprocess() with scripted model outputs.
 
-def scheduler_config(num_blocks, budget=4096, max_seqs=4, eos=99):
+def scheduler_config(num_blocks, budget=4096, max_seqs=4, eos=99, kv_eviction="lru"):
     return SimpleNamespace(max_num_seqs=max_seqs, max_num_batched_tokens=budget, eos=eos, kvcache_block_size=BS,
-                           num_kvcache_blocks=num_blocks)
+                           num_kvcache_blocks=num_blocks, kv_eviction=kv_eviction)
 
 
 class SchedulerRun(Run):
@@ -552,6 +552,57 @@ def scheduler_decode_growth_and_preemption(api):
     return run.trace
 
 
+def random_workload(api, seed, eviction="lru", prefetch=False, save_on_release=False, budget=None, hybrid=None):
+    """A seeded stream of requests over shared documents, scheduled and decoded for 40 steps.
+
+    Documents of 1-5 full blocks share leading blocks with each other, so
+    requests hit GPU blocks, CPU entries or nothing; requests arrive at random
+    steps with a random tail and 1-3 output tokens. Pool size, token budget and
+    batch size vary with the seed.
+    """
+    import random
+
+    rng = random.Random(seed)
+    num_blocks = rng.randint(6, 14)
+    run = SchedulerRun(api, num_blocks, budget=rng.choice([512, 1024, 4096]), max_seqs=rng.randint(1, 4),
+                       kv_eviction=eviction)
+    run.attach(prefetch=prefetch, save_on_release=save_on_release, budget=budget, hybrid=hybrid)
+    base = 1000 + 100 * seed
+    documents = []
+    for d in range(4):
+        shared = documents[rng.randrange(len(documents))][:rng.randint(1, 2)] if documents and rng.random() < 0.6 else []
+        own = [base + 10 * d + i for i in range(rng.randint(1, 5) - len(shared))]
+        documents.append(shared + own)
+    for step in range(40):
+        for _ in range(rng.choice([0, 0, 1, 1, 2])):
+            doc = rng.choice(documents)
+            blocks = doc[:rng.randint(1, len(doc))]
+            tail = rng.randint(0, BS - 1) if rng.random() < 0.7 else 0
+            tokens = tokens_of(*blocks, tail=tail, tail_value=base + 90 + step)
+            if len(tokens) // BS + 2 < num_blocks:
+                run.add(tokens, max_tokens=rng.randint(1, 3), ignore_eos=True)
+        if not run.scheduler.is_finished():
+            run.tick(f"step {step}")
+        if step % 10 == 9:
+            run.snap(f"after step {step}")
+    return run.trace
+
+
+def _random_scenarios():
+    out = {}
+    for seed, options in enumerate([{}, {"eviction": "mru"}, {"prefetch": True, "save_on_release": True},
+                                    {"prefetch": True, "eviction": "mru"}, {"budget": 3},
+                                    {"save_on_release": True, "budget": 5, "eviction": "mru"},
+                                    {"prefetch": True, "hybrid": (1e-3, 1e-6, 0.0)},
+                                    {"hybrid": (1e-4, 1e-5, 1e-9), "save_on_release": True},
+                                    {"prefetch": True, "save_on_release": True, "budget": 4},
+                                    {}, {"eviction": "mru", "prefetch": True, "save_on_release": True},
+                                    {"prefetch": True, "hybrid": (5e-4, 2e-6, 0.0), "eviction": "mru"}]):
+        out[f"random_workload_{seed}"] = (lambda api, seed=seed, options=options:
+                                          random_workload(api, seed, **options))
+    return out
+
+
 SCENARIOS = {
     "admission_with_gpu_and_cpu_hits": admission_with_gpu_and_cpu_hits,
     "admission_mru": admission_mru,
@@ -568,6 +619,7 @@ SCENARIOS = {
     "scheduler_chunked_restore": scheduler_chunked_restore,
     "scheduler_copy_failure_rollback": scheduler_copy_failure_rollback,
     "scheduler_decode_growth_and_preemption": scheduler_decode_growth_and_preemption,
+    **_random_scenarios(),
 }
 
 
