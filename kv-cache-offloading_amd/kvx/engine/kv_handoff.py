@@ -71,37 +71,41 @@ def copy_tokens(to_host: bool, pool: torch.Tensor, table, count: int, kv: torch.
         host_scale = scale.view(-1, count, heads, 1)
     released = [None, None]  # per buffer: the event after the last work that read or wrote it
     dma.wait_stream(kernels)  # the pool's tokens, and the payload, are ready for the caller's queued work
-    for i, (first, end) in enumerate(groups):
-        n, k = end - first, i % 2
-        stage = stages[k][:n]
-        stage_scale = scale_stages[k][:n] if scale is not None else None
-        if to_host:
-            if released[k] is not None:
-                kernels.wait_event(released[k])  # its previous copy to the host has read it
-            if scale is None:
-                ops.gather_tokens(pool, table, count, stage, planes=(first, end))
+    try:
+        for i, (first, end) in enumerate(groups):
+            n, k = end - first, i % 2
+            stage = stages[k][:n]
+            stage_scale = scale_stages[k][:n] if scale is not None else None
+            if to_host:
+                if released[k] is not None:
+                    kernels.wait_event(released[k])  # its previous copy to the host has read it
+                if scale is None:
+                    ops.gather_tokens(pool, table, count, stage, planes=(first, end))
+                else:
+                    ops.gather_tokens_fp8(pool, table, count, stage, stage_scale, planes=(first, end))
+                dma.wait_event(kernels.record_event())
+                with torch.cuda.stream(dma):
+                    host[first:end].copy_(stage, non_blocking=True)
+                    if scale is not None:
+                        host_scale[first:end].copy_(stage_scale, non_blocking=True)
+                released[k] = dma.record_event()
             else:
-                ops.gather_tokens_fp8(pool, table, count, stage, stage_scale, planes=(first, end))
-            dma.wait_event(kernels.record_event())
-            with torch.cuda.stream(dma):
-                host[first:end].copy_(stage, non_blocking=True)
-                if scale is not None:
-                    host_scale[first:end].copy_(stage_scale, non_blocking=True)
-            released[k] = dma.record_event()
-        else:
-            if released[k] is not None:
-                dma.wait_event(released[k])  # its previous scatter has read it
-            with torch.cuda.stream(dma):
-                stage.copy_(host[first:end], non_blocking=True)
-                if scale is not None:
-                    stage_scale.copy_(host_scale[first:end], non_blocking=True)
-            kernels.wait_event(dma.record_event())
-            if scale is None:
-                ops.scatter_tokens(pool, table, count, stage, planes=(first, end))
-            else:
-                ops.scatter_tokens_fp8(pool, table, count, stage, stage_scale, planes=(first, end))
-            released[k] = kernels.record_event()
-    kernels.wait_stream(dma)
+                if released[k] is not None:
+                    dma.wait_event(released[k])  # its previous scatter has read it
+                with torch.cuda.stream(dma):
+                    stage.copy_(host[first:end], non_blocking=True)
+                    if scale is not None:
+                        stage_scale.copy_(host_scale[first:end], non_blocking=True)
+                kernels.wait_event(dma.record_event())
+                if scale is None:
+                    ops.scatter_tokens(pool, table, count, stage, planes=(first, end))
+                else:
+                    ops.scatter_tokens_fp8(pool, table, count, stage, stage_scale, planes=(first, end))
+                released[k] = kernels.record_event()
+    finally:
+        # The staging is freed on return; later allocations on this stream must follow every DMA, also when
+        # a call above raised.
+        kernels.wait_stream(dma)
     kernels.synchronize()
 
 
