@@ -1053,7 +1053,12 @@ int kvx_cache_restore(kvx_cache* c, const int32_t* slots, const int32_t* ids, in
       if (!rc && base == 0) rc = c->wait_stream(s, compute);
       if (!rc) rc = wait_victims(base, cnt);
       if (!rc) rc = c->launch(false, ids + base, c->restore_staging, nullptr, cnt, s);
-      if (rc) return rc;
+      if (rc) {
+        // Earlier chunks are queued with no event the caller could order on,
+        // and the caller frees these blocks on an error: let them land first.
+        if (base > 0) (void)hipStreamSynchronize(s);
+        return rc;
+      }
     }
   }
   Event* done = nullptr;
@@ -1063,6 +1068,7 @@ int kvx_cache_restore(kvx_cache* c, const int32_t* slots, const int32_t* ids, in
   if (!rc && wait && s != compute) rc = c->queue_wait(compute, done);
   if (rc) {
     if (done) c->release_if_unused(done);
+    (void)hipStreamSynchronize(s);  // the restore is queued; the caller frees its blocks on an error
     return rc;
   }
   for (int32_t i = 0; i < n; ++i) {
