@@ -222,11 +222,13 @@ int kvx_cache_save(kvx_cache* cache, const int32_t* block_ids_host, const int32_
  * kvx_cache_save without attached staging and without allocation. It has no
  * counterpart in the reference: it is for callers that cannot allocate
  * (serving loops and harnesses that forbid hipMalloc, or processes whose
- * device memory all belongs to the KV pool). Ordering, results and errors
- * are those of kvx_cache_save, except that entries are staged in a static
- * array of KVX_NOALLOC_SCRATCH_BYTES that the library holds on each device
- * until the process ends, and that the call creates no events and allocates
- * no host or device memory. n may not exceed the entries that array holds,
+ * device memory all belongs to the KV pool). Results and errors are those
+ * of kvx_cache_save, and so are its ordering rules, except that it records a
+ * single event after its copies to host memory: a restore into a block it
+ * saved waits for those copies, not only for the save kernel. Entries are
+ * staged in a static array of KVX_NOALLOC_SCRATCH_BYTES that the library
+ * holds on each device until the process ends, and the call creates no
+ * events and allocates no host or device memory. n may not exceed the entries that array holds,
  * min(128, KVX_NOALLOC_SCRATCH_BYTES / entry_stride) (three Qwen3-8B FP8
  * entries); a larger n fails with KVX_E_RANGE before any work is queued.
  * Every such call on one device shares its array: calls queued on one save
