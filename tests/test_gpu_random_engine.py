@@ -43,17 +43,19 @@ def holds(pool, block_id, tokens, start, fp8, scale_dtype) -> str | None:
     return None
 
 
-def run_stream(gpu, seed, fp8, split, batched, options, monkeypatch):
+def run_stream(gpu, seed, fp8, split, batched, options, monkeypatch, heads=2, head_dim=128,
+               scale_dtype=torch.float32):
     rng = random.Random(seed)
     num_blocks = rng.randint(8, 14)
-    pool = torch.zeros((2, 2, num_blocks, BS, 2, 128), dtype=torch.bfloat16, device=gpu)
+    pool = torch.zeros((2, 2, num_blocks, BS, heads, head_dim), dtype=torch.bfloat16, device=gpu)
     engine = LLMEngine(SyntheticKVRunner(pool), max_num_batched_tokens=rng.choice([512, 1024, 4096]),
                        max_num_seqs=rng.randint(1, 4), eos=-1, kvcache_block_size=BS,
                        num_kvcache_blocks=num_blocks, kv_eviction=options.get("eviction", "lru"))
-    scale_dtype = torch.float32 if fp8 else None
+    scale_dtype = scale_dtype if fp8 else None
     if not batched:
         monkeypatch.setattr(CPUBlockCache, "coalesce", lambda self: nullcontext())
-    entry = 2 * 2 * BS * 2 * (128 + 4 if fp8 else 256)  # bytes per CPU entry
+    rows = 2 * 2 * BS * heads
+    entry = rows * (head_dim + scale_dtype.itemsize if fp8 else 2 * head_dim)  # bytes per CPU entry
     cache = engine.create_cpu_prefix_cache(rng.randint(3, 12) * entry, automatic=True, split_streams=split, fp8=fp8,
                                            scale_dtype=scale_dtype, prefetch=options.get("prefetch", False),
                                            save_on_release=options.get("save_on_release", False),
@@ -121,3 +123,18 @@ def test_random_request_streams_keep_every_block_intact(gpu, fp8, split, batched
     assert totals["requests"] > 0 and totals["saved"] > 0 and totals["restored"] > 0
     if fp8:
         assert totals["fp8"] > 0  # some verified blocks came back from FP8 entries
+
+
+@pytest.mark.parametrize("heads,head_dim,scale_dtype", [(4, 64, torch.float32), (1, 96, torch.float32),
+                                                        (2, 128, torch.bfloat16), (1, 256, torch.bfloat16)])
+@pytest.mark.parametrize("fp8", [True, False], ids=["fp8", "bf16"])
+def test_random_request_streams_on_other_head_shapes_and_scales(gpu, heads, head_dim, scale_dtype, fp8, monkeypatch):
+    # head_dim 96 takes the generic kernels (one thread per row) and staged restores only.
+    totals = {"exact": 0, "fp8": 0, "requests": 0}
+    for seed in range(4):
+        counts, _ = run_stream(gpu, seed, fp8, True, True, {"prefetch": True, "save_on_release": True},
+                               monkeypatch, heads, head_dim, scale_dtype)
+        for key in totals:
+            totals[key] += counts[key]
+    print(totals)
+    assert totals["requests"] > 0 and (totals["fp8"] > 0 or not fp8)
