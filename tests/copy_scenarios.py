@@ -14,14 +14,17 @@ BlockManager and CPUBlockCache do with the reference's hooks (block_manager.py:9
   restore with wait=True into it, without before_block_reuse, then a read;
 - use: before_block_use, then the caller's stream reads the block;
 - release-time saves of blocks that stay on the GPU (deallocate, inside coalesce());
-- discards of CPU entries: the slot can be reused by the next save while a restore still reads it.
+- discards of CPU entries: the slot can be reused by the next save while a restore still reads it;
+- with `switch_streams=True`, a change of the caller's current stream between actions, the new one first
+  waiting for the old one, as a correct torch program switches streams (the engine then sees copies and
+  waits issued for different caller streams).
 With `batched=False` nothing is coalesced, as with the reference's BlockManager (one engine call per
 block). The caller records what a sequential execution gives: every read of the caller's stream and the
 final value of every block and live slot. `check()` compares them with what the backend observed.
 
 A backend provides `batcher`, `write(block, value)` and `read(block) -> token` on the caller's stream,
-`value(token)` after `sync()`, `between()` (host time between calls), and `block_value` / `slot_value`
-after `sync()`. Values are the integers 1, 2, 3, ...
+`value(token)` after `sync()`, `between()` (host time between calls), `block_value` / `slot_value`
+after `sync()`, and `switch_stream()` if streams are switched. Values are the integers 1, 2, 3, ...
 """
 
 import random
@@ -29,9 +32,10 @@ import random
 
 class Caller:
     def __init__(self, rng: random.Random, backend, num_blocks: int, num_slots: int, batched: bool = True,
-                 max_request_blocks: int = 6):
+                 max_request_blocks: int = 6, switch_streams: bool = False):
         self.rng, self.backend = rng, backend
         self.batched = batched
+        self.switch_streams = switch_streams
         self.num_blocks = num_blocks
         self.max_request = max_request_blocks
         self.next_value = 1
@@ -161,10 +165,15 @@ class Caller:
         self.free_slots.append(slot)
         self.log.append(f"discard slot {slot}")
 
+    def switch_stream(self):
+        self.backend.switch_stream()
+        self.log.append("switch stream")
+
     ACTIONS = (("admission", 4), ("prefetch", 2), ("restore_block", 2), ("use", 3), ("release", 2), ("discard", 2))
 
     def run(self, rounds: int):
-        names, weights = zip(*self.ACTIONS)
+        actions = self.ACTIONS + ((("switch_stream", 2),) if self.switch_streams else ())
+        names, weights = zip(*actions)
         for _ in range(rounds):
             getattr(self, self.rng.choices(names, weights)[0])()
             self.backend.between()

@@ -26,24 +26,30 @@ BLOCKS, SLOTS, ROUNDS = 12, 10, 60
 class ModelBackend:
     def __init__(self, seed: int, split: bool, staging: int, kernel_reads: bool = True, debug: int = 0,
                  batcher=_CopyBatcher, noalloc: bool = False):
-        self.dev = Device(random.Random(seed * 7919 + 1), (COMPUTE, "save", "restore"))
+        self.dev = Device(random.Random(seed * 7919 + 1), (COMPUTE, "caller 2", "save", "restore"))
+        self.current = COMPUTE
         self.mem = Memory(BLOCKS, SLOTS)
         self.engine = ModelEngine(self.dev, self.mem, split, staging, kernel_reads, debug)
         engine = self.engine
         if noalloc:
             engine = NoAllocSaves(self.engine, lambda ids, slots, compute: self.engine.save(ids, slots, compute, True),
                                   self.engine.static_entries)
-        self.batcher = batcher(engine, lambda: COMPUTE)
+        self.batcher = batcher(engine, lambda: self.current)
+
+    def switch_stream(self):
+        new = "caller 2" if self.current == COMPUTE else COMPUTE
+        self.dev.wait(new, self.dev.record(self.current))
+        self.current = new
 
     def write(self, block, value):
         def op():
             self.mem.blocks[block] = value
 
-        self.dev.run(COMPUTE, op)
+        self.dev.run(self.current, op)
 
     def read(self, block):
         box = []
-        self.dev.run(COMPUTE, lambda: box.append(self.mem.blocks[block]))
+        self.dev.run(self.current, lambda: box.append(self.mem.blocks[block]))
         return box
 
     def value(self, token):
@@ -62,9 +68,10 @@ class ModelBackend:
         return self.mem.slots[slot]
 
 
-def run(seed, split, staging, batched=True, kernel_reads=True, debug=0, batcher=_CopyBatcher, noalloc=False):
+def run(seed, split, staging, batched=True, kernel_reads=True, debug=0, batcher=_CopyBatcher, noalloc=False,
+        switch_streams=False):
     backend = ModelBackend(seed, split, staging, kernel_reads, debug, batcher, noalloc)
-    caller = Caller(random.Random(seed), backend, BLOCKS, SLOTS, batched=batched)
+    caller = Caller(random.Random(seed), backend, BLOCKS, SLOTS, batched=batched, switch_streams=switch_streams)
     caller.run(ROUNDS)
     return caller.check(), caller, backend
 
@@ -97,6 +104,16 @@ def test_allocation_free_saves_keep_the_sequential_result(split, staging, batche
         assert not bad, f"seed {seed}: {bad[:5]}\n" + "\n".join(caller.log[-40:])
         paths.update(backend.engine.calls)
     assert ("save", "staged", "fixed") in paths and ("save", "direct", "fixed") in paths
+
+
+@pytest.mark.parametrize("split,staging,batched", [(True, 2, True), (True, 1, False), (False, 3, True),
+                                                   (False, 1, False)])
+def test_caller_stream_switches_keep_the_sequential_result(split, staging, batched):
+    # The caller moves between two streams, each switch ordered after the previous stream (as torch code does):
+    # kernel-read restores and waits land on either stream, saves reuse slots those restores read.
+    for seed in range(40):
+        bad, caller, _ = run(seed, split, staging, batched, switch_streams=True)
+        assert not bad, f"seed {seed}: {bad[:5]}\n" + "\n".join(caller.log[-40:])
 
 
 def fails_somewhere(seeds=60, **kwargs) -> bool:

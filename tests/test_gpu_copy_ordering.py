@@ -8,8 +8,8 @@ restore stream or the caller's stream, so copies lag behind the caller's work, o
 copies. Every read the caller's stream makes, and every block and live entry at the end, must hold what
 a sequential execution gives. The CPU model (test_copy_ordering_model.py) explores the interleavings;
 this runs the same sequences on the hardware, FP8 and BF16 entries, split streams and one copy stream,
-batched and one call per block, and with saves of up to 4 blocks through the allocation-free entry point
-(kvx_cache_save_noalloc).
+batched and one call per block, with saves of up to 4 blocks through the allocation-free entry point
+(kvx_cache_save_noalloc), and with the caller switching between two streams.
 """
 
 import random
@@ -69,6 +69,7 @@ class GpuBackend:
             engine = NoAllocSaves(self.engine, save_noalloc, 4)
         self.batcher = _CopyBatcher(engine, lambda: torch.cuda.current_stream(device).cuda_stream)
         self.reads = torch.empty((ROUNDS * 8 + 8, *self.pool[:, :, 0].shape), dtype=torch.bfloat16, device=device)
+        self.caller_streams = [torch.cuda.current_stream(device), torch.cuda.Stream(device)]
         self.n_reads = 0
         self.decode = {}  # bf16 bits -> value id
 
@@ -87,6 +88,12 @@ class GpuBackend:
         self.n_reads += 1
         self.reads[i].copy_(self.pool[:, :, block])
         return i
+
+    def switch_stream(self):
+        current = torch.cuda.current_stream(self.device)
+        new = self.caller_streams[1] if current == self.caller_streams[0] else self.caller_streams[0]
+        new.wait_stream(current)
+        torch.cuda.set_stream(new)
 
     def between(self):
         if self.rng.random() < 0.5:
@@ -119,18 +126,20 @@ class GpuBackend:
         return self._decode((codes * scales).to(torch.bfloat16))
 
     def close(self):
+        torch.cuda.set_stream(self.caller_streams[0])
         self.engine.close()
 
 
 @pytest.mark.parametrize("fmt", [ops.FORMAT_FP8, ops.FORMAT_RAW], ids=["fp8", "bf16"])
-@pytest.mark.parametrize("split,staging,batched,noalloc", [(True, 3, True, False), (True, 1, False, False),
-                                                           (False, 2, True, False), (True, 128, True, False),
-                                                           (True, 3, True, True), (False, 1, False, True)])
-def test_random_caller_sequences_give_the_sequential_result(gpu, fmt, split, staging, batched, noalloc):
+@pytest.mark.parametrize("split,staging,batched,noalloc,switch", [
+    (True, 3, True, False, False), (True, 1, False, False, False), (False, 2, True, False, False),
+    (True, 128, True, False, False), (True, 3, True, True, False), (False, 1, False, True, False),
+    (True, 2, True, False, True), (False, 1, False, False, True)])
+def test_random_caller_sequences_give_the_sequential_result(gpu, fmt, split, staging, batched, noalloc, switch):
     for seed in range(6):
         backend = GpuBackend(gpu, seed, fmt, split, staging, noalloc)
         try:
-            caller = Caller(random.Random(seed), backend, BLOCKS, SLOTS, batched=batched)
+            caller = Caller(random.Random(seed), backend, BLOCKS, SLOTS, batched=batched, switch_streams=switch)
             caller.run(ROUNDS)
             bad = caller.check()
             assert not bad, f"seed {seed}: {bad[:5]}\n" + "\n".join(caller.log[-30:])
