@@ -3,8 +3,9 @@
 Each test drops exactly one rule (kvx_cache_set_debug) in a scenario where a
 delay kernel on one copy stream lets the unordered access overtake the other,
 and asserts that the bytes come out wrong in at least one of a few attempts.
-The matching positive tests (test_gpu_cache.py, test_gpu_engine.py) pass with
-every rule in place, so these show those tests would catch a missing wait.
+The same scenarios pass with every rule in place (the last tests here), as do
+the matching positive tests (test_gpu_cache.py, test_gpu_engine.py), so these
+show those tests would catch a missing wait.
 The reference claims such controls (README.md:114-117) but commits none.
 """
 
@@ -72,14 +73,14 @@ def shows_race(scenario, *args):
     return any(scenario(*args) for _ in range(ATTEMPTS))
 
 
-def restore_without_save_wait(gpu):
+def restore_without_save_wait(gpu, debug=_lib.DEBUG_SKIP_SAVE_WAIT):
     pool = pool_with_bytes(gpu, 3)
     manager = BlockManager(3, BS)
     key = publish(manager, 0, 1)
     cache = cache_for(pool, manager, 1, split_streams=True, preallocate=True)
     cache._slab_memory[0].fill_(0xAB)
     expected = block(pool, 0)
-    cache._engine.set_debug(_lib.DEBUG_SKIP_SAVE_WAIT)
+    cache._engine.set_debug(debug)
     delay(cache._copy_stream, gpu)
     assert cache.save_block(key)
     forget(manager, key)
@@ -99,7 +100,7 @@ def test_restore_reads_a_poisoned_slot_without_the_save_wait(gpu):
     assert shows_race(restore_without_save_wait, gpu)
 
 
-def reuse_without_reuse_wait(gpu, compute):
+def reuse_without_reuse_wait(gpu, compute, debug=_lib.DEBUG_SKIP_REUSE_WAIT):
     """One save delayed on the copy stream, then a compute-stream write with the reuse wait dropped."""
     pool = pool_with_bytes(gpu, 2)
     manager = BlockManager(2, BS)
@@ -107,7 +108,7 @@ def reuse_without_reuse_wait(gpu, compute):
     with torch.cuda.stream(compute):
         cache = cache_for(pool, manager, 1)
         expected = block(pool, 1)
-        cache._engine.set_debug(_lib.DEBUG_SKIP_REUSE_WAIT)
+        cache._engine.set_debug(debug)
         delay(cache._copy_stream, gpu)
         assert cache.save_block(key)
         forget(manager, key)
@@ -126,7 +127,7 @@ def test_compute_overwrites_a_block_before_its_save_without_the_reuse_wait(gpu):
     assert any(reuse_without_reuse_wait(gpu, s) for s in candidates)
 
 
-def restore_without_victim_wait(gpu):
+def restore_without_victim_wait(gpu, debug=_lib.DEBUG_SKIP_VICTIM_WAIT):
     pool = pool_with_bytes(gpu, 2)
     manager = BlockManager(2, BS)
     victim_key = publish(manager, 0, 3)
@@ -136,7 +137,7 @@ def restore_without_victim_wait(gpu):
     assert cache.save_block(key)
     cache.synchronize()
     forget(manager, key)
-    cache._engine.set_debug(_lib.DEBUG_SKIP_VICTIM_WAIT)
+    cache._engine.set_debug(debug)
     original = cache._save_to_slot
 
     def slow_save(block_id, slot):
@@ -158,7 +159,7 @@ def test_restore_overwrites_a_victim_before_its_save_without_the_victim_wait(gpu
     assert shows_race(restore_without_victim_wait, gpu)
 
 
-def save_without_slot_read_wait(gpu):
+def save_without_slot_read_wait(gpu, debug=_lib.DEBUG_SKIP_SLOT_READ_WAIT):
     pool = pool_with_bytes(gpu, 3)
     manager = BlockManager(3, BS)
     key_a = publish(manager, 0, 5)
@@ -167,7 +168,7 @@ def save_without_slot_read_wait(gpu):
     assert cache.save_block(key_a)
     cache.synchronize()
     forget(manager, key_a)
-    cache._engine.set_debug(_lib.DEBUG_SKIP_SLOT_READ_WAIT)
+    cache._engine.set_debug(debug)
     entry = cache._entries[key_a]
     manager.free_block_ids = deque([2, 0, 1])
     delay(cache._restore_stream, gpu)
@@ -206,3 +207,24 @@ def test_a_save_overwrites_a_slot_another_callers_stream_still_reads_without_the
     from test_gpu_cache import slot_reuse_across_caller_streams
 
     assert shows_race(lambda device: not slot_reuse_across_caller_streams(device, _lib.DEBUG_SKIP_SLOT_READ_WAIT), gpu)
+
+
+@pytest.mark.parametrize("scenario", [restore_without_save_wait, restore_without_victim_wait,
+                                      save_without_slot_read_wait], ids=lambda f: f.__name__)
+def test_each_scenario_keeps_its_bytes_with_every_rule_in_place(gpu, scenario):
+    # The same scenarios with no rule dropped: no attempt may show a race.
+    assert not any(scenario(gpu, 0) for _ in range(ATTEMPTS))
+
+
+def test_the_reuse_scenario_keeps_its_bytes_with_every_rule_in_place(gpu):
+    candidates = [torch.cuda.default_stream(gpu)] + [torch.cuda.Stream(gpu) for _ in range(ATTEMPTS - 1)]
+    assert not any(reuse_without_reuse_wait(gpu, s, 0) for s in candidates)
+
+
+@pytest.mark.parametrize("scenario", ["chunked_recycle", "waited_restore_over_prefetch",
+                                      "slot_reuse_across_caller_streams"])
+def test_the_engine_level_scenarios_keep_their_bytes_with_every_rule_in_place(gpu, scenario):
+    # As often as their controls run them, each time on fresh streams.
+    import test_gpu_cache
+
+    assert all(getattr(test_gpu_cache, scenario)(gpu) for _ in range(ATTEMPTS))
