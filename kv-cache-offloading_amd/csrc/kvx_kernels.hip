@@ -85,12 +85,13 @@ __device__ __forceinline__ uint32_t load_host32(__amdgpu_buffer_rsrc_t r, int of
 // beats it for the restore and store_kvcache kernels. The save kernel alone
 // gains ~1% with runs of 1024 tiles, but a restore launched after such a save
 // ran 0.4-0.5% slower, so the save keeps one eighth per XCD too. The BF16
-// copies gain ~1.5% with runs of 64 tiles (one 512 KiB plane).
+// copies, with 1 KiB tiles, are fastest in the dispatcher's own order (0).
 constexpr int kXcds = 8;
 constexpr int kSaveXcdRun = -1;
-constexpr int kCopyXcdRun = 64;
+constexpr int kCopyXcdRun = 0;
 template <int kChunk = -1>
 __device__ __forceinline__ int xcd_tile(int bid, int grid) {
+  if (kChunk == 0) return bid;  // the dispatcher's own round-robin order
   if (kChunk < 0) {
     const int per = grid / kXcds;
     if (bid >= per * kXcds) return bid;  // the ragged tail keeps its place
@@ -496,13 +497,19 @@ __global__ __launch_bounds__(kThreads) void fp8_restore_generic(uint16_t* __rest
 // ---------------------------------------------------------------------------
 // RAW (BF16 mode) gather / scatter: byte copies of each block plane.
 
-// uint4 per thread per tile. Device-side copies use 8 KiB tiles with
-// nontemporal loads and stores: on 128 Qwen3-8B blocks, gather 5.93 -> 6.23
-// and scatter 5.83 -> 6.22 TB/s against 16 KiB tiles with plain loads
-// (4 KiB tiles from 128 threads: 6.27 gather). Striding copies to or from
-// host memory keep 16 KiB tiles: their few workgroups need the larger tiles
-// in flight to keep the host link busy.
-constexpr int kCopyVecs = 2;
+// Tile shape of the device-side copies: one nontemporal 16-byte piece per
+// thread in 64-thread workgroups (1 KiB tiles), taken in the dispatcher's
+// order. Measured on 128 Qwen3-8B blocks (TB/s, gather / scatter, median of
+// two passes): 6.71 / 6.62, against 6.28 / 6.31 for 8 KiB tiles of 256
+// threads in 64-tile runs per XCD, 6.59 / 6.58 for 1 KiB tiles in one
+// contiguous eighth per XCD, 6.34 / 6.33 for 2 KiB tiles of 128 threads and
+// 5.45 / 5.53 for 2 KiB tiles of 64 threads. A plain 1:1 streaming copy of
+// the same bytes reaches 6.63-6.73 (hipMemcpyAsync device to device: 4.25).
+// Striding copies to or from host memory keep 16 KiB tiles of 256 threads:
+// their few workgroups need the larger tiles in flight to keep the host link
+// busy.
+constexpr int kCopyThreads = 64;
+constexpr int kCopyVecs = 1;
 constexpr int kStrideCopyVecs = 4;
 
 // Entry e receives plane p of its block at entries[e] + p * entry_plane_stride;
@@ -510,13 +517,13 @@ constexpr int kStrideCopyVecs = 4;
 // copies last_bytes (a sequence's partial final block in a token gather).
 // kStride: copies to or from host memory by a capped striding grid, as the
 // FP8 kernels' striding instances; writes to host memory use system-scope stores.
-template <bool kToEntry, bool kStride>
-__global__ __launch_bounds__(kThreads) void raw_copy_kernel(uint8_t* __restrict__ pool, PlaneGeom g,
-                                                           BlockBatch b, int64_t plane_bytes,
-                                                           int64_t elem_bytes, int64_t entry_plane_stride,
-                                                           int64_t last_bytes) {
+template <bool kToEntry, bool kStride, int kBlock = kStride ? kThreads : kCopyThreads>
+__global__ __launch_bounds__(kBlock) void raw_copy_kernel(uint8_t* __restrict__ pool, PlaneGeom g,
+                                                         BlockBatch b, int64_t plane_bytes,
+                                                         int64_t elem_bytes, int64_t entry_plane_stride,
+                                                         int64_t last_bytes) {
   constexpr int kVecs = kStride ? kStrideCopyVecs : kCopyVecs;
-  constexpr int kTileBytes = kThreads * kVecs * 16;
+  constexpr int kTileBytes = kBlock * kVecs * 16;
   const int per_entry = g.planes * g.chunks;
   const int tiles = kStride ? b.n * per_entry : 1;
   for (int t = kStride ? (int)blockIdx.x : 0; t < tiles; t += kStride ? (int)gridDim.x : 1) {
@@ -533,7 +540,7 @@ __global__ __launch_bounds__(kThreads) void raw_copy_kernel(uint8_t* __restrict_
   uint4 v[kVecs];
 #pragma unroll
   for (int k = 0; k < kVecs; ++k) {
-    const int64_t off = off0 + ((int64_t)k * kThreads + threadIdx.x) * 16;
+    const int64_t off = off0 + ((int64_t)k * kBlock + threadIdx.x) * 16;
     if (kStride && !kToEntry)  // from host memory; past `valid` the resource reads zeros
       v[k] = load_host16(host_rsrc(src + off0, valid - off0), (int)(off - off0));
     else
@@ -541,7 +548,7 @@ __global__ __launch_bounds__(kThreads) void raw_copy_kernel(uint8_t* __restrict_
   }
 #pragma unroll
   for (int k = 0; k < kVecs; ++k) {
-    const int64_t off = off0 + ((int64_t)k * kThreads + threadIdx.x) * 16;
+    const int64_t off = off0 + ((int64_t)k * kBlock + threadIdx.x) * 16;
     if (off < valid) store16<kStride && kToEntry>(dst + off, v[k]);
   }
   }
@@ -790,14 +797,14 @@ static hipError_t launch_raw(bool to_entry, void* pool, const kvx_block_layout& 
   const bool vec = vector_ok && plane_bytes % 16 == 0 && entry_plane_stride % 16 == 0 && last_bytes % 16 == 0;
   const int64_t es = l.elem_bytes;
   if (vec) {
-    auto tiled = [&](int vecs) {
-      const int64_t tile_bytes = (int64_t)kThreads * vecs * 16;
+    auto tiled = [&](int threads, int vecs) {
+      const int64_t tile_bytes = (int64_t)threads * vecs * 16;
       PlaneGeom g = make_geom(l, 0, 0);
       g.chunks = (int32_t)((plane_bytes + tile_bytes - 1) / tile_bytes);
       return g;
     };
     if (max_grid > 0) {
-      const PlaneGeom g = tiled(kStrideCopyVecs);
+      const PlaneGeom g = tiled(kThreads, kStrideCopyVecs);
       if ((unsigned)max_grid < (unsigned)(b.n * g.planes * g.chunks)) {
         if (to_entry)
           hipLaunchKernelGGL((raw_copy_kernel<true, true>), dim3((unsigned)max_grid), dim3(kThreads), 0, stream,
@@ -808,14 +815,14 @@ static hipError_t launch_raw(bool to_entry, void* pool, const kvx_block_layout& 
         return hipGetLastError();
       }
     }
-    const PlaneGeom g = tiled(kCopyVecs);
+    const PlaneGeom g = tiled(kCopyThreads, kCopyVecs);
     const unsigned grid = (unsigned)(b.n * g.planes * g.chunks);
     if (to_entry)
-      hipLaunchKernelGGL((raw_copy_kernel<true, false>), dim3(grid), dim3(kThreads), 0, stream, (uint8_t*)pool, g, b,
-                         plane_bytes, es, entry_plane_stride, last_bytes);
-    else
-      hipLaunchKernelGGL((raw_copy_kernel<false, false>), dim3(grid), dim3(kThreads), 0, stream, (uint8_t*)pool, g,
+      hipLaunchKernelGGL((raw_copy_kernel<true, false>), dim3(grid), dim3(kCopyThreads), 0, stream, (uint8_t*)pool, g,
                          b, plane_bytes, es, entry_plane_stride, last_bytes);
+    else
+      hipLaunchKernelGGL((raw_copy_kernel<false, false>), dim3(grid), dim3(kCopyThreads), 0, stream, (uint8_t*)pool,
+                         g, b, plane_bytes, es, entry_plane_stride, last_bytes);
   } else {
     PlaneGeom g = make_geom(l, 0, 0);
     const unsigned grid = generic_grid((int64_t)b.n * l.planes * (plane_bytes / 2));
