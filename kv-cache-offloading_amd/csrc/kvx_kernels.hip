@@ -578,24 +578,30 @@ __global__ __launch_bounds__(kThreads) void raw_copy_generic(uint8_t* __restrict
 // ---------------------------------------------------------------------------
 // store_kvcache (nanovllm/layers/attention.py:10-30)
 
-// Rows of kRow16 uint4; 256 threads cover kTok = 256 / (2 * kRow16) tokens
-// (K row then V row), one 16-byte load and store per thread. Small workgroups
-// with one access each, nontemporal accesses and XCD-contiguous token ranges
-// were the fastest shape on the 16-sequence Qwen3-8B batch (random slots:
-// 4.77 -> 5.29 TB/s; contiguous slots: 4.85 -> 5.89 TB/s); several passes per
-// workgroup were slower.
+// Rows of kRow16 uint4: each thread moves one 16-byte piece of a token's K
+// row or V row, kStoreThreads consecutive pieces per workgroup. One access
+// per thread, nontemporal accesses and XCD-contiguous token ranges were the
+// fastest shape on the 16-sequence Qwen3-8B batch (random slots: 4.77 -> 5.29
+// TB/s; contiguous slots: 4.85 -> 5.89 TB/s); several passes per workgroup
+// were slower. Workgroup size and order, as fractions of 8 TB/s (random /
+// paged-block / contiguous slots, two passes agreeing within 0.1 point):
+// 128 threads in eighths 67.2 / 75.1 / 76.4; 256 in eighths 66.6 / 74.3 /
+// 75.4; 64 in eighths 66.9 / 75.0 / 76.2; 64 in dispatch order 66.7 / 75.5 /
+// 77.6; 64 in 64-workgroup runs 65.0 / 71.2 / 75.0.
+constexpr int kStoreThreads = 128;
+constexpr int kStoreXcdRun = -1;
 template <int kRow16>
-__global__ __launch_bounds__(kThreads) void store_kv_vec(const uint4* __restrict__ key, int64_t key_stride16,
-                                                        const uint4* __restrict__ value, int64_t value_stride16,
-                                                        uint4* __restrict__ k_cache, uint4* __restrict__ v_cache,
-                                                        const int32_t* __restrict__ slots, int64_t n,
-                                                        int64_t cache_slots) {
-  constexpr int kTok = kThreads / (2 * kRow16);
-  static_assert(kTok >= 1, "row too long for one workgroup");
-  const int within = threadIdx.x % (2 * kRow16);
+__global__ __launch_bounds__(kStoreThreads) void store_kv_vec(const uint4* __restrict__ key, int64_t key_stride16,
+                                                             const uint4* __restrict__ value, int64_t value_stride16,
+                                                             uint4* __restrict__ k_cache, uint4* __restrict__ v_cache,
+                                                             const int32_t* __restrict__ slots, int64_t n,
+                                                             int64_t cache_slots) {
+  // 16-byte piece p of the batch: token p / (2 kRow16), then its K row and its V row.
+  const int64_t p = (int64_t)xcd_tile<kStoreXcdRun>(blockIdx.x, gridDim.x) * kStoreThreads + threadIdx.x;
+  const int64_t t = p / (2 * kRow16);
+  const int within = (int)(p - t * (2 * kRow16));
   const bool is_v = within >= kRow16;
   const int col = is_v ? within - kRow16 : within;
-  const int64_t t = (int64_t)xcd_tile(blockIdx.x, gridDim.x) * kTok + threadIdx.x / (2 * kRow16);
   if (t >= n) return;
   const int64_t slot = slots[t];
   if (slot < 0 || slot >= cache_slots) return;
@@ -892,10 +898,9 @@ hipError_t launch_store_kvcache(const void* key, int64_t key_stride, const void*
   const bool aligned = ((uintptr_t)key | (uintptr_t)value | (uintptr_t)k_cache | (uintptr_t)v_cache) % 16 == 0 &&
                        ks % 16 == 0 && vs % 16 == 0 && row_bytes % 16 == 0;
   auto vec = [&](auto kernel, int row16) {
-    const int64_t tok = kThreads / (2 * row16);
-    const int64_t grid = (n + tok - 1) / tok;
+    const int64_t grid = (n * 2 * row16 + kStoreThreads - 1) / kStoreThreads;
     if (grid > INT32_MAX) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(kThreads), 0, stream, (const uint4*)key, ks / 16,
+    hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(kStoreThreads), 0, stream, (const uint4*)key, ks / 16,
                        (const uint4*)value, vs / 16, (uint4*)k_cache, (uint4*)v_cache, slot_mapping, n,
                        cache_slots);
     return hipGetLastError();
