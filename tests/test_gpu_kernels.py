@@ -202,8 +202,11 @@ def byte_pattern_pool(device, shape=(2, 3, 9, 256, 2, 64)):
     return pool
 
 
-@pytest.mark.parametrize("shape", [(2, 3, 9, 256, 2, 64), (2, 2, 5, 256, 1, 4), (2, 1, 4, 3, 1, 3)])
+@pytest.mark.parametrize("shape", [(2, 3, 9, 256, 2, 64), (2, 2, 5, 256, 1, 4), (2, 1, 4, 3, 1, 3),
+                                   (2, 2, 5, 16, 1, 8), (2, 2, 6, 24, 3, 8)])
 def test_bf16_block_gather_and_scatter_are_byte_exact(gpu, shape):
+    # Planes of 64 KiB and 2 KiB fill whole 1 KiB copy tiles; 256 B and 1,152 B planes end in a partial tile; 18 B
+    # planes take the 2-byte generic kernel.
     pool = byte_pattern_pool(gpu, shape)
     layout = ops.pool_layout(pool)
     _, _, stride = ops.entry_layout(layout, ops.FORMAT_RAW)
