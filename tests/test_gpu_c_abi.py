@@ -45,3 +45,28 @@ def test_a_plain_c_program_saves_and_restores_through_the_c_abi(gpu, tmp_path):
     assert np.array_equal(after_raw[:, :, 1], after_fp8[:, :, 5])
     for b in (0, 2, 3, 5):
         assert np.array_equal(after_raw[:, :, b], after_fp8[:, :, b])
+
+
+STRESS = Path(__file__).resolve().parent / "c_abi" / "engine_stress"
+
+
+def run_stress(seed: int, split: int, debug: int = 0, iterations: int = 1500) -> tuple[int, str]:
+    assert STRESS.exists(), "build() compiles tests/c_abi/engine_stress.c"
+    proc = subprocess.run([str(STRESS), str(seed), str(iterations), str(split), str(debug)], capture_output=True,
+                          text=True, timeout=120)
+    assert proc.returncode in (0, 4), proc.stdout + proc.stderr  # 4: mismatches, every call succeeded
+    line = proc.stdout.strip().splitlines()[-1]
+    return int(line.split()[0]), proc.stdout
+
+
+@pytest.mark.parametrize("seed,split", [(1, 1), (2, 1), (3, 0), (4, 0)])
+def test_a_random_c_workload_keeps_every_block_and_slot_intact(gpu, seed, split):
+    mismatches, out = run_stress(seed, split)
+    assert mismatches == 0, out
+
+
+@pytest.mark.parametrize("flag", [_lib.DEBUG_SKIP_SAVE_WAIT, _lib.DEBUG_SKIP_SLOT_READ_WAIT,
+                                  _lib.DEBUG_SKIP_REUSE_WAIT, _lib.DEBUG_SKIP_VICTIM_WAIT])
+def test_the_c_workload_catches_a_dropped_ordering_rule(gpu, flag):
+    # Negative control for the test above (split streams): with one rule dropped, some seed's checkpoints fail.
+    assert any(run_stress(seed, 1, flag)[0] > 0 for seed in (1, 2, 3))
