@@ -478,7 +478,7 @@ def hybrid_leg(torch, pool, scale_dtype, prefix_blocks=128):
     return out
 
 
-def agent_leg(torch, pool, scale_dtype):
+def agent_leg(torch, pool, scale_dtype, h2d_gbs=None):
     """Agent pressure through the whole engine: 4 agents x 32,768-token contexts, 12 turns of 2,048 new tokens.
 
     FP8 saves of evicted blocks into an 8 GiB pinned budget, restores and
@@ -496,6 +496,15 @@ def agent_leg(torch, pool, scale_dtype):
     334-340), and from then on the run only restores. `budget_for_all` repeats
     the split-stream run with a budget that holds every agent's blocks, so
     saves continue through every turn.
+
+    Each agent's request hints the next agent's prefix with
+    prefetch_prefix(defer=True): the engine starts those restores right after
+    the request's admission, so they overlap its compute. `hints_after_first_step`
+    repeats the split-stream run hinting after the request's first step, the
+    only time a client of the reference engine can hint (its hints are dropped
+    while a request waits). With `h2d_gbs` (the copy engine's measured H2D rate
+    for batched restores), each run reports the time its H2D bytes need at
+    that rate and its wall time over it.
     """
     from contextlib import nullcontext
 
@@ -508,10 +517,12 @@ def agent_leg(torch, pool, scale_dtype):
     blocks_per_agent = -(-(32768 + 12 * (2048 + 1)) // pool.shape[3])
     entry = 2 * pool.shape[1] * pool.shape[3] * pool.shape[4] * (pool.shape[5] + scale_dtype.itemsize)
     budget_for_all = -(-4 * blocks_per_agent * entry // (1 << 30)) << 30  # every agent's blocks, in whole GiB
-    runs = (("warm-up", True, 1, True, budget), ("split_streams", True, 12, True, budget),
-            ("one_copy_stream", False, 12, True, budget), ("per_block_calls", True, 12, False, budget),
-            ("budget_for_all", True, 12, True, budget_for_all))
-    for name, split, turns, batched, max_bytes in runs:
+    runs = (("warm-up", True, 1, True, budget, "deferred"), ("split_streams", True, 12, True, budget, "deferred"),
+            ("hints_after_first_step", True, 12, True, budget, "after_first_step"),
+            ("one_copy_stream", False, 12, True, budget, "deferred"),
+            ("per_block_calls", True, 12, False, budget, "deferred"),
+            ("budget_for_all", True, 12, True, budget_for_all, "deferred"))
+    for name, split, turns, batched, max_bytes, hints in runs:
         engine = LLMEngine(SyntheticKVRunner(pool), max_num_batched_tokens=16384, max_num_seqs=4, eos=-1,
                            kvcache_block_size=pool.shape[3], num_kvcache_blocks=pool.shape[2])
         cache = engine.create_cpu_prefix_cache(max_bytes, automatic=True, prefetch=True, split_streams=split,
@@ -520,7 +531,8 @@ def agent_leg(torch, pool, scale_dtype):
             cache.coalesce = nullcontext  # the block manager then issues one engine call per block
         try:
             with marked(f"agents: {name}"):
-                r = run_agent_pressure(engine, agents=4, context=32768, turns=turns, append=2048, verify=False)
+                r = run_agent_pressure(engine, agents=4, context=32768, turns=turns, append=2048, verify=False,
+                                       hints=hints)
         finally:
             engine.exit()
         if name == "warm-up":
@@ -529,7 +541,14 @@ def agent_leg(torch, pool, scale_dtype):
                      "restored_blocks": r.restored_blocks, "prefetched_blocks": r.prefetched_blocks,
                      "d2h_bytes": r.d2h_bytes, "h2d_bytes": r.h2d_bytes, "link_gbs": round(r.link_gbs, 2),
                      "host_blocked_s": round(r.host_blocked_s, 3), "drain_s": round(r.drain_s, 4),
-                     "budget_skips": r.budget_skips, "host_budget_bytes": max_bytes}
+                     "budget_skips": r.budget_skips, "host_budget_bytes": max_bytes, "hints": hints}
+        if h2d_gbs:
+            floor = r.h2d_bytes / (h2d_gbs * 1e9)
+            out[name].update(h2d_floor_s=round(floor, 3), wall_over_h2d_floor=round(r.wall_s / floor, 3))
+        log(f"agents {name}: {json.dumps(out[name])}")
+    if h2d_gbs:
+        out["h2d_gbs_for_floor"] = h2d_gbs
+    out["deferred_hint_speedup"] = round(out["hints_after_first_step"]["wall_s"] / out["split_streams"]["wall_s"], 3)
     out["split_speedup"] = round(out["one_copy_stream"]["wall_s"] / out["split_streams"]["wall_s"], 3)
     out["batching_speedup"] = round(out["per_block_calls"]["wall_s"] / out["split_streams"]["wall_s"], 3)
     return out
@@ -1044,16 +1063,50 @@ def headline_leg(torch, pool, layout, sources, dests, steps, warmup):
         engine.close()
 
 
+def profiler_tool_loaded(maps_path="/proc/self/maps"):
+    """The rocprofiler-sdk library mapped into this process, if one is (a rocprofv3 run loads it), else None."""
+    try:
+        with open(maps_path) as maps:
+            for line in maps:
+                if "librocprofiler-sdk" in line:
+                    return line.split()[-1]
+    except OSError:
+        return None
+    return None
+
+
+# Copiers whose copies may still be in flight after a timed-out wait: their buffers and signals must outlive them.
+_ABANDONED_COPIERS = []
+
+
 class SdmaCopier:
     """Copies between a device buffer and pinned host memory on explicitly chosen SDMA engines, through HSA's
     hsa_amd_memory_async_copy_on_engine, bypassing the HIP runtime's choice of engine (it runs device-to-host
-    hipMemcpyAsync copies as blit kernels). `unavailable` names why it cannot run on this machine, if it cannot."""
+    hipMemcpyAsync copies as blit kernels). `unavailable` names why it cannot run here, if it cannot.
+
+    The copier owns one hsa_init reference and every signal it creates. close() (or leaving a `with` block)
+    destroys the signals and calls hsa_shut_down, so the process never ends with HSA state of the probe's
+    making. A copy that fails to queue leaves no signal behind: the pieces queued before it are waited for
+    first. A wait that times out leaves its copies possibly in flight, so their signals and buffers are then
+    kept until the process ends, and HSA stays initialised.
+
+    It refuses to run under a profiler tool (rocprofiler-sdk mapped into the process): a traced run that
+    queued these copies ended in a segmentation fault during the tool's teardown, and the tracer intercepts
+    exactly these HSA calls.
+    """
 
     def __init__(self, torch, nbytes, piece=64 << 20):
         import re
 
         self.unavailable = None
+        self.hsa = None
+        self.abandoned = False
+        self._live = []
         self.nbytes, self.piece = nbytes, piece
+        tool = profiler_tool_loaded()
+        if tool:
+            self.unavailable = f"a profiler tool is loaded ({tool}); explicit SDMA copies are not run under it"
+            return
         try:
             hsa = ctypes.CDLL("libhsa-runtime64.so.1")
         except OSError as error:
@@ -1061,12 +1114,14 @@ class SdmaCopier:
             return
         u64, u32 = ctypes.c_uint64, ctypes.c_uint32
         hsa.hsa_init.restype = ctypes.c_int
+        hsa.hsa_shut_down.restype = ctypes.c_int
         hsa.hsa_iterate_agents.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
         hsa.hsa_agent_get_info.argtypes = [u64, ctypes.c_int, ctypes.c_void_p]
         hsa.hsa_signal_create.argtypes = [ctypes.c_int64, u32, ctypes.c_void_p, ctypes.POINTER(u64)]
         hsa.hsa_signal_destroy.argtypes = [u64]
         hsa.hsa_signal_load_scacquire.argtypes = [u64]
         hsa.hsa_signal_load_scacquire.restype = ctypes.c_int64
+        hsa.hsa_signal_subtract_screlease.argtypes = [u64, ctypes.c_int64]
         hsa.hsa_amd_memory_copy_engine_status.argtypes = [u64, u64, ctypes.POINTER(u32)]
         hsa.hsa_amd_memory_async_copy_on_engine.argtypes = [ctypes.c_void_p, u64, ctypes.c_void_p, u64,
                                                             ctypes.c_size_t, u32, ctypes.c_void_p, u64, ctypes.c_int,
@@ -1120,62 +1175,99 @@ class SdmaCopier:
         torch.cuda.synchronize()
         self.pieces = [(off, min(piece, nbytes - off)) for off in range(0, nbytes, piece)]
 
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
     def start(self, directions, spread=1):
         """Queues every piece of each direction ("d2h", "h2d"), alternating over `spread` engines per direction;
-        returns the completion signals."""
+        returns the completion signals. If a piece fails to queue, the copies queued so far are waited for
+        and every signal of the call is destroyed before the error is raised."""
+        if self.unavailable or self.abandoned:
+            raise RuntimeError(f"SDMA copier cannot queue copies: {self.unavailable or 'a wait timed out'}")
         hsa, signals = self.hsa, []
-        for direction in directions:
-            sig = ctypes.c_uint64()
-            if hsa.hsa_signal_create(len(self.pieces), 0, None, ctypes.byref(sig)) != 0:
-                raise RuntimeError("hsa_signal_create failed")
-            signals.append(sig.value)
-            engines = self.engines[direction][:spread]
-            for i, (off, size) in enumerate(self.pieces):
-                engine = engines[i % len(engines)]
-                if direction == "d2h":
-                    rc = hsa.hsa_amd_memory_async_copy_on_engine(self.host_dst.data_ptr() + off, self.cpu,
-                                                                 self.dev_src.data_ptr() + off, self.gpu, size, 0,
-                                                                 None, sig.value, engine, True)
-                else:
-                    rc = hsa.hsa_amd_memory_async_copy_on_engine(self.dev_dst.data_ptr() + off, self.gpu,
-                                                                 self.host_src.data_ptr() + off, self.cpu, size, 0,
-                                                                 None, sig.value, engine, True)
-                if rc != 0:
-                    raise RuntimeError(f"hsa_amd_memory_async_copy_on_engine ({direction}) returned {rc}")
+        try:
+            for direction in directions:
+                sig = ctypes.c_uint64()
+                if hsa.hsa_signal_create(len(self.pieces), 0, None, ctypes.byref(sig)) != 0:
+                    raise RuntimeError("hsa_signal_create failed")
+                signals.append(sig.value)
+                self._live.append(sig.value)
+                engines = self.engines[direction][:spread]
+                for i, (off, size) in enumerate(self.pieces):
+                    engine = engines[i % len(engines)]
+                    if direction == "d2h":
+                        rc = hsa.hsa_amd_memory_async_copy_on_engine(self.host_dst.data_ptr() + off, self.cpu,
+                                                                     self.dev_src.data_ptr() + off, self.gpu, size,
+                                                                     0, None, sig.value, engine, True)
+                    else:
+                        rc = hsa.hsa_amd_memory_async_copy_on_engine(self.dev_dst.data_ptr() + off, self.gpu,
+                                                                     self.host_src.data_ptr() + off, self.cpu, size,
+                                                                     0, None, sig.value, engine, True)
+                    if rc != 0:
+                        # The pieces not queued never decrement the signal: take them off its count.
+                        hsa.hsa_signal_subtract_screlease(sig.value, len(self.pieces) - i)
+                        raise RuntimeError(f"hsa_amd_memory_async_copy_on_engine ({direction}) returned {rc}")
+        except BaseException:
+            if signals:
+                self.wait(signals)  # copies already queued still write the buffers
+            raise
         return signals
 
     def wait(self, signals, limit_s=30.0):
+        """Waits for the signals to reach zero, then destroys them. On a timeout the copies may still run: the
+        signals are kept and the copier takes no more work."""
         deadline = time.perf_counter() + limit_s
         while any(self.hsa.hsa_signal_load_scacquire(sig) > 0 for sig in signals):
             if time.perf_counter() > deadline:
+                self.abandoned = True
                 raise RuntimeError(f"SDMA copies did not finish within {limit_s} s")
             time.sleep(20e-6)
         for sig in signals:
             self.hsa.hsa_signal_destroy(sig)
+            self._live.remove(sig)
 
     def run(self, directions, spread=1):
         t0 = time.perf_counter()
         self.wait(self.start(directions, spread))
         return time.perf_counter() - t0
 
+    def close(self):
+        """Destroys the remaining signals and balances hsa_init, unless a wait timed out (see the class)."""
+        if self.hsa is None:
+            return
+        if self.abandoned:
+            _ABANDONED_COPIERS.append(self)
+            return
+        for sig in self._live:
+            self.hsa.hsa_signal_destroy(sig)
+        self._live.clear()
+        for name in ("dev_src", "dev_dst", "host_dst", "host_src"):
+            self.__dict__.pop(name, None)
+        hsa, self.hsa = self.hsa, None
+        hsa.hsa_shut_down()
+
 
 def sdma_probe(torch, nbytes, reps=3):
     """Plain DMA duplex over the host link on explicit SDMA engines: D2H alone, H2D alone, both at once, each on
     one engine and spread over two. GB/s, or why it could not run."""
-    copier = SdmaCopier(torch, nbytes)
-    if copier.unavailable:
-        return {"skipped": copier.unavailable}
-    out = {"bytes_per_direction": nbytes, "piece_bytes": copier.piece, "engines": copier.engines,
-           "engine_masks": copier.masks}
-    try:
-        for name, directions, spread in (("d2h", ["d2h"], 1), ("h2d", ["h2d"], 1), ("duplex", ["d2h", "h2d"], 1),
-                                         ("d2h_2_engines", ["d2h"], 2), ("h2d_2_engines", ["h2d"], 2),
-                                         ("duplex_2_engines_each", ["d2h", "h2d"], 2)):
-            best = min(copier.run(directions, spread) for _ in range(reps))
-            out[f"{name}_gbs"] = round(len(directions) * nbytes / best / 1e9, 2)
-    except RuntimeError as error:
-        out["error"] = str(error)
-    return out
+    with SdmaCopier(torch, nbytes) as copier:
+        if copier.unavailable:
+            return {"skipped": copier.unavailable}
+        out = {"bytes_per_direction": nbytes, "piece_bytes": copier.piece, "engines": copier.engines,
+               "engine_masks": copier.masks}
+        try:
+            for name, directions, spread in (("d2h", ["d2h"], 1), ("h2d", ["h2d"], 1),
+                                             ("duplex", ["d2h", "h2d"], 1), ("d2h_2_engines", ["d2h"], 2),
+                                             ("h2d_2_engines", ["h2d"], 2),
+                                             ("duplex_2_engines_each", ["d2h", "h2d"], 2)):
+                best = min(copier.run(directions, spread) for _ in range(reps))
+                out[f"{name}_gbs"] = round(len(directions) * nbytes / best / 1e9, 2)
+        except RuntimeError as error:
+            out["error"] = str(error)
+        return out
 
 
 def interference_leg(torch, nbytes=1 << 30, reps=20, kvx_kernels=None):
@@ -1227,17 +1319,19 @@ def interference_leg(torch, nbytes=1 << 30, reps=20, kvx_kernels=None):
 
     out = {"streams_concurrent": concurrent, "copy_bytes": nbytes,
            "sdma": copier.unavailable or "available"}
-    for name, work in {f"{reps} x torch.add over 512 MiB bf16": adds, **(kvx_kernels or {})}.items():
-        kernels_ms(work=work)
-        res = {"alone_ms": round(kernels_ms(work=work), 3)}
-        with marked(f"interference: {name} beside runtime D2H"):
-            res["beside_runtime_d2h_ms"] = round(kernels_ms(runtime_copy(2), work=work), 3)
-        with marked(f"interference: {name} beside runtime H2D"):
-            res["beside_runtime_h2d_ms"] = round(kernels_ms(runtime_copy(1), work=work), 3)
-        if not copier.unavailable:
-            with marked(f"interference: {name} beside SDMA D2H"):
-                res["beside_sdma_d2h_ms"] = round(kernels_ms(lambda: copier.start(["d2h"]), copier.wait, work), 3)
-        out[name] = res
+    with copier:
+        for name, work in {f"{reps} x torch.add over 512 MiB bf16": adds, **(kvx_kernels or {})}.items():
+            kernels_ms(work=work)
+            res = {"alone_ms": round(kernels_ms(work=work), 3)}
+            with marked(f"interference: {name} beside runtime D2H"):
+                res["beside_runtime_d2h_ms"] = round(kernels_ms(runtime_copy(2), work=work), 3)
+            with marked(f"interference: {name} beside runtime H2D"):
+                res["beside_runtime_h2d_ms"] = round(kernels_ms(runtime_copy(1), work=work), 3)
+            if not copier.unavailable:
+                with marked(f"interference: {name} beside SDMA D2H"):
+                    res["beside_sdma_d2h_ms"] = round(kernels_ms(lambda: copier.start(["d2h"]), copier.wait,
+                                                                 work), 3)
+            out[name] = res
     return out
 
 
@@ -1485,7 +1579,8 @@ def main():
         result["hybrid_admission"] = hybrid_leg(torch, pool, scale_dtype)
     if not args.skip_agents:
         log("agent pressure leg")
-        result["agent_pressure"] = agent_leg(torch, pool, scale_dtype)
+        h2d_gbs = result["host_link"].get("legs", {}).get("restore_h2d_gbs")
+        result["agent_pressure"] = agent_leg(torch, pool, scale_dtype, h2d_gbs)
     if not args.skip_cpu_baseline:
         log("cpu baseline leg")
         result["cpu_baseline"] = cpu_baseline_leg(torch, pool, sources, dests, scale_dtype, inventory)

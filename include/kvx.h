@@ -34,7 +34,14 @@
 extern "C" {
 #endif
 
-#define KVX_ABI_VERSION 1
+/*
+ * Version 2: kvx_upload and kvx_cache_dma_counters; allocation-free saves of
+ * different caches on one device ordered by a per-device event; staging areas
+ * replaced on a split-stream cache order both copy streams; waited one- and
+ * two-block restores may run on the caller's stream; synchronize/destroy wait
+ * for those; set_staging rejects overlapping split areas; KVX_DEBUG_* flags.
+ */
+#define KVX_ABI_VERSION 2
 
 /* Error codes (negative); positive values are hipError_t. */
 #define KVX_OK 0
@@ -187,6 +194,9 @@ int kvx_cache_destroy(kvx_cache* cache);
  * Pass the same pointer twice when split_streams == 0; with split streams the
  * two areas may not overlap (KVX_E_INVALID). Copies already queued keep
  * using the previous areas, which must stay allocated until they complete.
+ * When a split-stream cache's areas change, each copy stream first waits for
+ * the work already queued on the other, so a previous area may become the
+ * other stream's new one without a race.
  */
 int kvx_cache_set_staging(kvx_cache* cache, void* save_staging, void* restore_staging,
                           int32_t entries);
@@ -231,9 +241,12 @@ int kvx_cache_save(kvx_cache* cache, const int32_t* block_ids_host, const int32_
  * events and allocates no host or device memory. n may not exceed the entries that array holds,
  * min(128, KVX_NOALLOC_SCRATCH_BYTES / entry_stride) (three Qwen3-8B FP8
  * entries); a larger n fails with KVX_E_RANGE before any work is queued.
- * Every such call on one device shares its array: calls queued on one save
- * stream run in order, but calls of different caches (different save
- * streams) that overlap in time race and produce wrong bytes.
+ * Every such call on one device shares its array. Calls are ordered by one
+ * event per device, created with the device's first cache: each call's save
+ * stream waits for the previous call's copies out of the array, whichever
+ * cache made it, and the calls are issued one at a time (a per-device
+ * mutex). Calls of different caches therefore follow each other on the
+ * device in the order they were made.
  */
 int kvx_cache_save_noalloc(kvx_cache* cache, const int32_t* block_ids_host, const int32_t* slots_host,
                            int32_t n, void* compute_stream);
@@ -265,6 +278,16 @@ int kvx_cache_synchronize(kvx_cache* cache);
 /* Counts of engine activity: saves, restores, waits inserted; for tests and stats. */
 int kvx_cache_counters(kvx_cache* cache, int64_t* saved_blocks, int64_t* restored_blocks,
                        int64_t* stream_waits);
+/*
+ * DMA transfers the engine has queued (hipMemcpyAsync calls, each at most
+ * 64 MiB) and their bytes, per direction. Saves and restores that the kernels
+ * move over the host link themselves queue none. A memory-copy trace of the
+ * engine's work holds exactly these copies; comparing the counts shows
+ * whether the tracer lost records. No reference counterpart (the reference's
+ * copies are torch copy_ calls).
+ */
+int kvx_cache_dma_counters(kvx_cache* cache, int64_t* d2h_copies, int64_t* d2h_bytes, int64_t* h2d_copies,
+                           int64_t* h2d_bytes);
 
 /*
  * Negative controls (tests only): each flag drops one ordering rule so a test
@@ -284,6 +307,24 @@ int kvx_cache_counters(kvx_cache* cache, int64_t* saved_blocks, int64_t* restore
 #define KVX_DEBUG_SKIP_VICTIM_WAIT 8
 #define KVX_DEBUG_SKIP_OVERWRITE_WAIT 16
 int kvx_cache_set_debug(kvx_cache* cache, int32_t flags);
+
+/* Largest kvx_upload. */
+#define KVX_UPLOAD_MAX_BYTES (1LL << 30)
+
+/*
+ * Copies nbytes from pinned, device-accessible host memory (hipHostMalloc;
+ * torch's pin_memory) to device memory by a kernel queued on `stream`, in
+ * place of the pinned non-blocking host-to-device copies of a step's inputs
+ * (token ids, positions, slot_mapping: nanovllm/engine/model_runner.py:
+ * 169-173, 187-190). A DMA copy queued there waits behind every
+ * host-to-device DMA already queued on the device, a restore stream's bulk
+ * copies included; the kernel does not. The source is read when the kernel
+ * runs: it must stay allocated and unchanged until then. Both ends of
+ * [src_pinned, src_pinned + nbytes) must lie in one pinned host allocation
+ * (KVX_E_INVALID otherwise) and nbytes may not exceed KVX_UPLOAD_MAX_BYTES
+ * (KVX_E_RANGE). Graph-capturable.
+ */
+int kvx_upload(void* dst, const void* src_pinned, int64_t nbytes, void* stream);
 
 /*
  * Queues a kernel that keeps one wave busy for `microseconds` on `stream`

@@ -343,6 +343,13 @@ struct ScratchTable {
   bool looked_up[kMaxScratchDevices] = {};
   int status[kMaxScratchDevices] = {};        // KVX_OK, or the code of a failed lookup
   uint8_t* address[kMaxScratchDevices] = {};  // device address of `scratch` on each device
+  // Per device: the latest allocation-free save's copies out of the array
+  // (recorded on that save's stream), and a mutex held while a call queues
+  // its wait, its work and the new record, so calls of different caches
+  // follow each other in the order they are made.
+  std::mutex use_mu[kMaxScratchDevices];
+  hipEvent_t last_use[kMaxScratchDevices] = {};
+  hipStream_t last_stream[kMaxScratchDevices] = {};
 };
 
 ScratchTable g_scratch;
@@ -358,7 +365,8 @@ void scratch_setup(int device, uint8_t** address, int* status) {
   std::lock_guard<std::mutex> lock(g_scratch.mu);
   if (!g_scratch.looked_up[device]) {
     void* p = nullptr;
-    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err == hipSuccess) err = hipEventCreateWithFlags(&g_scratch.last_use[device], hipEventDisableTiming);
     if (err != hipSuccess) {
       (void)hipGetLastError();  // leave no error behind for the caller's next HIP call
       g_scratch.status[device] = (int)err;
@@ -400,6 +408,7 @@ struct kvx_cache {
   std::vector<std::pair<hipStream_t, Event*>> caller_reads;
   bool host_reads_ok = false;  // restores may read host slots with the striding kernel
   int64_t saved = 0, restored = 0, waits = 0;
+  int64_t d2h_copies = 0, d2h_bytes = 0, h2d_copies = 0, h2d_bytes = 0;  // DMA transfers queued
   int32_t debug = 0;  // KVX_DEBUG_* negative-control flags
   // kvx_cache_save_noalloc: the device's static staging and the status of its
   // lookup, and the one event every such save records (created with the
@@ -628,6 +637,8 @@ struct kvx_cache {
         hipError_t err = to_host ? hipMemcpyAsync(h0 + off, d + off, n, hipMemcpyDeviceToHost, s)
                                  : hipMemcpyAsync(d + off, h0 + off, n, hipMemcpyHostToDevice, s);
         if (err != hipSuccess) return hip_status(err, to_host ? "D2H hipMemcpyAsync" : "H2D hipMemcpyAsync");
+        ++(to_host ? d2h_copies : h2d_copies);
+        (to_host ? d2h_bytes : h2d_bytes) += (int64_t)n;
       }
       i = j;
     }
@@ -822,6 +833,39 @@ int kvx_scatter_tokens_fp8(void* pool, const kvx_block_layout* layout, const int
                    const_cast<void*>(scales), (hipStream_t)stream);
 }
 
+int kvx_upload(void* dst, const void* src_pinned, int64_t nbytes, void* stream) {
+  if (nbytes < 0) return set_error(KVX_E_INVALID, "negative byte count");
+  if (nbytes > KVX_UPLOAD_MAX_BYTES)
+    return set_error(KVX_E_RANGE, "%lld bytes exceed the largest upload (%lld)", (long long)nbytes,
+                     (long long)KVX_UPLOAD_MAX_BYTES);
+  if (nbytes == 0) return KVX_OK;
+  if (!dst || !src_pinned) return set_error(KVX_E_INVALID, "NULL destination or source");
+  // The kernel reads the source through the device's mapping of it. Two
+  // independent checks that every byte read lies in one pinned allocation:
+  // the first and last bytes are both pinned host memory, mapped nbytes - 1
+  // apart, and the allocation holding the first byte extends past the last.
+  hipPointerAttribute_t head, tail;
+  const uint8_t* last = (const uint8_t*)src_pinned + (nbytes - 1);
+  if (hipPointerGetAttributes(&head, src_pinned) != hipSuccess || hipPointerGetAttributes(&tail, last) != hipSuccess ||
+      head.type != hipMemoryTypeHost || tail.type != hipMemoryTypeHost || !head.devicePointer ||
+      (uintptr_t)tail.devicePointer - (uintptr_t)head.devicePointer != (uintptr_t)(nbytes - 1)) {
+    (void)hipGetLastError();
+    return set_error(KVX_E_INVALID, "the upload source is not %lld bytes of pinned, device-accessible host memory",
+                     (long long)nbytes);
+  }
+  hipDeviceptr_t base = nullptr;
+  size_t size = 0;
+  if (hipMemGetAddressRange(&base, &size, head.devicePointer) != hipSuccess) {
+    (void)hipGetLastError();
+    return set_error(KVX_E_INVALID, "the upload source's allocation could not be looked up");
+  }
+  const uintptr_t start = (uintptr_t)head.devicePointer, first = (uintptr_t)base;
+  if (start < first || start - first + (uint64_t)nbytes > (uint64_t)size)
+    return set_error(KVX_E_INVALID, "the upload source runs past its pinned allocation (%lld of %llu bytes left)",
+                     (long long)(first + size - start), (unsigned long long)size);
+  return hip_status(launch_upload(dst, head.devicePointer, nbytes, (hipStream_t)stream), "upload kernel launch");
+}
+
 int kvx_sleep(void* stream, int64_t microseconds) {
   if (microseconds < 0 || microseconds > 60LL * 1000 * 1000)
     return set_error(KVX_E_RANGE, "sleep must be within [0, 60 s]");
@@ -910,6 +954,16 @@ int kvx_cache_set_staging(kvx_cache* c, void* save_staging, void* restore_stagin
   const uintptr_t save_at = (uintptr_t)save_staging, restore_at = (uintptr_t)restore_staging;
   if (c->split && save_at < restore_at + (uintptr_t)staging_bytes && restore_at < save_at + (uintptr_t)staging_bytes)
     return set_error(KVX_E_INVALID, "split streams need save and restore staging buffers that do not overlap");
+  // Copies queued on one stream may still use an area that becomes the other
+  // stream's: each stream's later copies wait for the other's queued work.
+  if (c->split && c->save_staging &&
+      ((uint8_t*)save_staging != c->save_staging || (uint8_t*)restore_staging != c->restore_staging)) {
+    DeviceScope scope;
+    int rc = scope.enter(c->device);
+    if (!rc) rc = c->wait_stream(c->restore_stream, c->save_stream);
+    if (!rc) rc = c->wait_stream(c->save_stream, c->restore_stream);
+    if (rc) return rc;
+  }
   c->save_staging = (uint8_t*)save_staging;
   c->restore_staging = (uint8_t*)restore_staging;
   c->staging_entries = entries;
@@ -971,8 +1025,25 @@ int kvx_cache_save_noalloc(kvx_cache* c, const int32_t* ids, const int32_t* slot
   if (n > max_n)
     return set_error(KVX_E_RANGE, "%d blocks exceed the static staging: at most %d entries of %lld bytes fit in %lld "
                      "bytes", n, max_n, (long long)c->entry_stride, (long long)KVX_NOALLOC_SCRATCH_BYTES);
-  return save_blocks_to_slots(c, ids, slots, n, (hipStream_t)compute_stream, c->static_staging, max_n,
-                              c->static_done);
+  // The array is the device's, not the cache's: wait for the previous call's
+  // copies out of it unless stream order already gives that.
+  std::lock_guard<std::mutex> lock(g_scratch.use_mu[c->device]);
+  hipEvent_t last_use = g_scratch.last_use[c->device];
+  hipStream_t& last_stream = g_scratch.last_stream[c->device];
+  DeviceScope scope;
+  rc = scope.enter(c->device);
+  if (rc) return rc;
+  if (last_stream && last_stream != c->save_stream) {
+    rc = hip_status(hipStreamWaitEvent(c->save_stream, last_use, 0), "hipStreamWaitEvent");
+    if (rc) return rc;
+    ++c->waits;
+  }
+  rc = save_blocks_to_slots(c, ids, slots, n, (hipStream_t)compute_stream, c->static_staging, max_n,
+                            c->static_done);
+  // Recorded even after a failure: work already queued may still use the array.
+  const int rc2 = hip_status(hipEventRecord(last_use, c->save_stream), "hipEventRecord");
+  if (rc2 == KVX_OK) last_stream = c->save_stream;
+  return rc ? rc : rc2;
 }
 
 int kvx_cache_restore(kvx_cache* c, const int32_t* slots, const int32_t* ids, int32_t n, int32_t wait,
@@ -1136,6 +1207,16 @@ int kvx_cache_counters(kvx_cache* c, int64_t* saved_blocks, int64_t* restored_bl
   if (saved_blocks) *saved_blocks = c->saved;
   if (restored_blocks) *restored_blocks = c->restored;
   if (stream_waits) *stream_waits = c->waits;
+  return KVX_OK;
+}
+
+int kvx_cache_dma_counters(kvx_cache* c, int64_t* d2h_copies, int64_t* d2h_bytes, int64_t* h2d_copies,
+                           int64_t* h2d_bytes) {
+  if (!c) return set_error(KVX_E_INVALID, "NULL cache");
+  if (d2h_copies) *d2h_copies = c->d2h_copies;
+  if (d2h_bytes) *d2h_bytes = c->d2h_bytes;
+  if (h2d_copies) *h2d_copies = c->h2d_copies;
+  if (h2d_bytes) *h2d_bytes = c->h2d_bytes;
   return KVX_OK;
 }
 

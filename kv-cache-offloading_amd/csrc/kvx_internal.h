@@ -91,6 +91,9 @@ hipError_t launch_store_kvcache(const void* key, int64_t key_stride, const void*
                                 int64_t value_stride, void* k_cache, void* v_cache,
                                 const int32_t* slot_mapping, int64_t num_tokens, int64_t row_elems,
                                 int32_t elem_bytes, int64_t cache_slots, hipStream_t stream);
+// Copies n bytes of pinned host memory at `src` (a device-accessible address)
+// to device memory at `dst` with a kernel on `stream`; n < 2^31.
+hipError_t launch_upload(void* dst, const void* src, int64_t n, hipStream_t stream);
 hipError_t launch_sleep(hipStream_t stream, int64_t microseconds);
 hipError_t launch_selftest(uint64_t* counters, hipStream_t stream);
 

@@ -630,6 +630,37 @@ __global__ __launch_bounds__(kThreads) void store_kv_generic(const T* __restrict
 // Test delay (bench/test_automatic_cpu_cache.py:47-48): one wave polls the
 // device wall clock until `ticks` have passed.
 
+// ---------------------------------------------------------------------------
+// Host-to-device uploads read by a kernel
+
+// A host-to-device copy queued on the caller's stream waits behind every
+// host-to-device DMA already queued on the device, whichever stream queued
+// it: on MI355X a 128 KiB pinned upload beside 2 GB of restore DMA on another
+// stream finished only when the DMA did (33.4 ms, against 0.04 ms alone). A
+// kernel on the caller's stream that reads the pinned source over the host
+// link leaves the DMA queue out. 16-byte system-scope loads when source and
+// destination allow them, else bytes; the buffer resource bounds every read
+// to [src, src + n).
+constexpr int kUploadThreads = 256;
+constexpr int kUploadMaxGrid = 64;
+
+template <bool kVec>
+__global__ __launch_bounds__(kUploadThreads) void upload_kernel(uint8_t* __restrict__ dst, const uint8_t* src,
+                                                               int64_t n) {
+  const __amdgpu_buffer_rsrc_t r = host_rsrc(src, n);
+  const int64_t first = (int64_t)blockIdx.x * kUploadThreads + threadIdx.x;
+  const int64_t step = (int64_t)gridDim.x * kUploadThreads;
+  int64_t done = 0;
+  if (kVec) {
+    const int64_t pieces = n / 16;
+    for (int64_t i = first; i < pieces; i += step)
+      *reinterpret_cast<uint4*>(dst + i * 16) = load_host16(r, (int)(i * 16));
+    done = pieces * 16;
+  }
+  for (int64_t i = done + first; i < n; i += step)
+    dst[i] = __builtin_amdgcn_raw_buffer_load_b8(r, (int)i, 0, kSystemScope);
+}
+
 __global__ void sleep_kernel(uint64_t ticks) {
   if (threadIdx.x != 0) return;
   const uint64_t t0 = wall_clock64();
@@ -930,6 +961,20 @@ hipError_t launch_store_kvcache(const void* key, int64_t key_stride, const void*
                        (const uint8_t*)value, vs, (uint8_t*)k_cache, (uint8_t*)v_cache, slot_mapping, row_bytes,
                        cache_slots);
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_upload(void* dst, const void* src, int64_t n, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  const bool vec = ((uintptr_t)dst | (uintptr_t)src) % 16 == 0;
+  const int64_t units = vec ? (n + 15) / 16 : n;
+  const unsigned grid = (unsigned)std::min<int64_t>(kUploadMaxGrid, (units + kUploadThreads - 1) / kUploadThreads);
+  if (vec)
+    hipLaunchKernelGGL(upload_kernel<true>, dim3(grid), dim3(kUploadThreads), 0, stream, (uint8_t*)dst,
+                       (const uint8_t*)src, n);
+  else
+    hipLaunchKernelGGL(upload_kernel<false>, dim3(grid), dim3(kUploadThreads), 0, stream, (uint8_t*)dst,
+                       (const uint8_t*)src, n);
   return hipGetLastError();
 }
 

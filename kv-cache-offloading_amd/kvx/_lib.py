@@ -14,7 +14,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must precede the dlopen below)
 
 LIB_PATH = Path(__file__).resolve().with_name("libkvx.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 E_INVALID, E_RANGE, E_STATE, E_UNSUPPORTED = -1, -2, -3, -4
 SCALE_BF16, SCALE_FP32 = 0, 1
@@ -22,6 +22,7 @@ FORMAT_RAW, FORMAT_FP8 = 0, 1
 DEBUG_SKIP_SAVE_WAIT, DEBUG_SKIP_SLOT_READ_WAIT, DEBUG_SKIP_REUSE_WAIT, DEBUG_SKIP_VICTIM_WAIT = 1, 2, 4, 8
 DEBUG_SKIP_OVERWRITE_WAIT = 16
 NOALLOC_SCRATCH_BYTES = 64 << 20  # KVX_NOALLOC_SCRATCH_BYTES
+UPLOAD_MAX_BYTES = 1 << 30  # KVX_UPLOAD_MAX_BYTES
 
 _c_p = ctypes.c_void_p
 _i32, _i64 = ctypes.c_int32, ctypes.c_int64
@@ -75,7 +76,10 @@ SIGNATURES = {
     "kvx_cache_before_block_use": (_i32, [_c_p, _i32, _c_p]),
     "kvx_cache_synchronize": (_i32, [_c_p]),
     "kvx_cache_counters": (_i32, [_c_p, ctypes.POINTER(_i64), ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
+    "kvx_cache_dma_counters": (_i32, [_c_p, ctypes.POINTER(_i64), ctypes.POINTER(_i64), ctypes.POINTER(_i64),
+                                      ctypes.POINTER(_i64)]),
     "kvx_cache_set_debug": (_i32, [_c_p, _i32]),
+    "kvx_upload": (_i32, [_c_p, _c_p, _i64, _c_p]),
     "kvx_sleep": (_i32, [_c_p, _i64]),
     "kvx_selftest": (_i32, [_c_p, _c_p]),
 }
@@ -103,13 +107,16 @@ def lib() -> ctypes.CDLL:
                     raise RuntimeError(f"libkvx is not built ({LIB_PATH} missing): run "
                                        "python kv-cache-offloading_amd/build.py")
                 handle = ctypes.CDLL(str(LIB_PATH))
+                # The version first: a library of another version may lack symbols bound below.
+                handle.kvx_abi_version.restype = _i32
+                version = handle.kvx_abi_version()
+                if version != ABI_VERSION:
+                    raise RuntimeError(f"libkvx ABI {version} does not match the binding's {ABI_VERSION}: "
+                                       "rebuild it with python kv-cache-offloading_amd/build.py")
                 for name, (restype, argtypes) in SIGNATURES.items():
                     fn = getattr(handle, name)
                     fn.restype = restype
                     fn.argtypes = argtypes
-                version = handle.kvx_abi_version()
-                if version != ABI_VERSION:
-                    raise RuntimeError(f"libkvx ABI {version} does not match the binding's {ABI_VERSION}")
                 _lib = handle
     return _lib
 

@@ -17,6 +17,7 @@ torch-op path for CPU-resident pools.
 """
 
 import ctypes
+import warnings
 from collections import Counter
 from contextlib import contextmanager
 from dataclasses import dataclass
@@ -118,6 +119,11 @@ class _CopyEngine:
         self.layout, self.fmt = layout, fmt
         self.logical_bytes, self.scale_offset, self.entry_stride = ops.entry_layout(layout, fmt)
         streams, self.streams_concurrent = _copy_streams(pool.device, 2 if split else 1)
+        if not self.streams_concurrent:
+            warnings.warn(f"no {'pair of copy streams' if split else 'copy stream'} found that runs beside the "
+                          "compute stream" + (" and each other" if split else "") + f" after {_STREAM_CANDIDATES} "
+                          "candidates: copies and compute will serialise (saves and restores at about half the "
+                          "duplex host-link rate)", RuntimeWarning, stacklevel=3)
         self.save_stream = streams[0]
         self.restore_stream = streams[-1]
         handle = ctypes.c_void_p()
@@ -153,6 +159,12 @@ class _CopyEngine:
         vals = [ctypes.c_int64() for _ in range(3)]
         check(lib().kvx_cache_counters(self.handle, *map(ctypes.byref, vals)), "kvx_cache_counters")
         return dict(zip(("saved_blocks", "restored_blocks", "stream_waits"), (v.value for v in vals)))
+
+    def dma_counters(self) -> dict[str, int]:
+        """DMA transfers queued so far (each at most 64 MiB) and their bytes, per direction."""
+        vals = [ctypes.c_int64() for _ in range(4)]
+        check(lib().kvx_cache_dma_counters(self.handle, *map(ctypes.byref, vals)), "kvx_cache_dma_counters")
+        return dict(zip(("d2h_copies", "d2h_bytes", "h2d_copies", "h2d_bytes"), (v.value for v in vals)))
 
     def set_debug(self, flags: int):
         """Negative controls for tests: drop ordering rules (kvx._lib.DEBUG_*); results become wrong."""
@@ -510,6 +522,22 @@ class CPUBlockCache:
     @property
     def stats(self) -> dict[str, int]:
         return {name: self._counts[name] for name in ("saved_blocks", "restored_blocks", "budget_skips")}
+
+    @property
+    def streams_concurrent(self) -> bool:
+        """False if the copy streams found run serialised with the compute stream or each other (a warning said so)."""
+        return self._engine.streams_concurrent
+
+    @property
+    def copy_stats(self) -> dict:
+        """The copy engine's own figures, beside the reference's `stats` (whose keys its tests compare whole):
+        whether the copy streams run concurrently, cross-stream waits queued, and DMA copies and bytes per
+        direction."""
+        self._require_open()
+        out = {"streams_concurrent": self._engine.streams_concurrent,
+               "stream_waits": self._engine.counters()["stream_waits"]}
+        out.update(self._engine.dma_counters())
+        return out
 
     def __len__(self):
         return len(self._entries)

@@ -103,17 +103,27 @@ class LLMEngine:
             split_streams=split_streams, fp8=fp8, hybrid=hybrid, scale_dtype=scale_dtype)
         return self._cpu_prefix_cache
 
-    def prefetch_prefix(self, prefix) -> int:
+    def prefetch_prefix(self, prefix, *, defer: bool = False) -> int:
         """Client hint that a request starting with `prefix` (token ids or a Sequence) arrives soon.
 
         Restores its CPU hits into free blocks beyond one per running request
         and returns how many it started; nothing while requests wait for
         admission, so a hint never takes blocks they need. Pass the same
         Sequence when repeating a hint (its block hashes are kept on it).
+
+        defer=True keeps a hint given while requests wait (replacing one kept
+        before) instead of dropping it. The next step that admits them starts
+        it right after their admissions, before the model runs, so the
+        hint's restores overlap that step's compute rather than following it.
+        The call then returns 0. A hint the engine can start now is started
+        now, whatever `defer` says.
         """
-        if self.scheduler.waiting:
+        if self.scheduler.waiting and not defer:
             return 0
         seq = prefix if isinstance(prefix, Sequence) else Sequence(prefix)
+        if self.scheduler.waiting:
+            self.scheduler.prefetch_hint = seq
+            return 0
         return self.scheduler.block_manager.prefetch(seq, reserve=len(self.scheduler.running))
 
     # -- KV handoff (llm_engine.py:128-173) ------------------------------------------------

@@ -12,6 +12,15 @@ restored span copies. A waiting request that does not fit sets
 tier) and prefetches its CPU hits into spare blocks, keeping one block per
 running request for decode growth (:101-107).
 
+A client hint kept for later (`prefetch_hint`, set by
+LLMEngine.prefetch_prefix(..., defer=True) while requests wait) is started
+at the end of the first prefill pass after which no waiting request lacks
+blocks: the step's admissions have taken theirs, and the model has not run
+yet, so the hint's restores overlap the step's compute. The reference
+starts hints only between steps (nanovllm/engine/llm_engine.py:112-126),
+where a hint given while a request waits is dropped and its restores begin
+after that request's compute.
+
 Decode gives each running request one token and a new block when it crosses
 a block boundary, preempting the newest running request (or itself) when no
 block is free.
@@ -72,6 +81,7 @@ class Scheduler:
                                           getattr(config, "kv_eviction", "lru"))
         self.waiting: deque[Sequence] = deque()
         self.running: deque[Sequence] = deque()
+        self.prefetch_hint: Sequence | None = None
 
     def is_finished(self) -> bool:
         return not self.waiting and not self.running
@@ -138,10 +148,25 @@ class Scheduler:
                     self._promote(seq, log)
                 elif not (seq.restore_span and reached == seq.restore_span[0]):
                     break  # chunked: it stays at the head of the queue
+            if batch and self.prefetch_hint is not None:
+                self._start_hint()
         except BaseException:
             log.rewind()
             raise
         return batch
+
+    def _start_hint(self):
+        """One attempt at the kept hint, once every waiting request holds its blocks; the hint is then dropped.
+
+        Requests that are still waiting here continue a chunked prefill or a
+        split head; each keeps a block, as running ones do, for the token it
+        samples. A failing copy raises out of the pass, which then rewinds
+        its admissions.
+        """
+        if any(not seq.block_table for seq in self.waiting):
+            return  # a request still needs blocks: the hint must not take them
+        hint, self.prefetch_hint = self.prefetch_hint, None
+        self.block_manager.prefetch(hint, reserve=len(self.running) + len(self.waiting))
 
     def _promote(self, seq: Sequence, log: _UndoLog):
         """The request's whole prompt is in this batch: it moves from waiting to running."""

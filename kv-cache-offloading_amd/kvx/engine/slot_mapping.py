@@ -5,10 +5,12 @@ view: block_table[position // block_size] * block_size + position % block_size
 (nanovllm/engine/model_runner.py:156-166 for prefill, :186 for decode; -1
 pads a captured graph's batch, :211). The producers build int32 numpy
 arrays with vectorised arithmetic (a 65K-token prefill is one pass, not a
-Python loop per token); `upload` moves one to the device the way the
-reference's runner does (:173, 189): a pinned host copy and a non-blocking
-host-to-device copy on the current stream, so the host never waits for the
-GPU to drain.
+Python loop per token); `upload` moves one to the device without waiting
+for the GPU, as the reference's runner does with a pinned host copy and a
+non-blocking host-to-device copy (:173, 189). Here a kernel on the current
+stream reads the pinned copy (kvx.ops.upload): a DMA copy there would queue
+behind the restore stream's bulk host-to-device copies, delaying the step by
+as long as the restores in flight take.
 """
 
 import numpy as np
@@ -42,6 +44,7 @@ def decode_slot_mapping(seqs, block_size: int, padded_to: int | None = None) -> 
 
 
 def upload(values: np.ndarray, device: torch.device) -> torch.Tensor:
-    """A device copy of a host array through pinned memory, queued without blocking the host."""
-    host = torch.from_numpy(np.ascontiguousarray(values)).pin_memory()
-    return host.to(device, non_blocking=True)
+    """A device copy of a host array, read from pinned memory by a kernel on the current stream."""
+    from kvx import ops
+
+    return ops.upload(values, device)

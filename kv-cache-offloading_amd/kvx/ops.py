@@ -8,8 +8,10 @@ torch-op fallback, so a missing or unloadable libkvx raises.
 """
 
 import ctypes
+import threading
 from math import prod
 
+import numpy as np
 import torch
 
 from kvx import _lib
@@ -198,6 +200,84 @@ def restore_blocks(pool: torch.Tensor, block_ids, entries, fmt: int, scale_dtype
     check(lib().kvx_restore_blocks(pool.data_ptr(), ctypes.byref(layout), fmt, int32_array(ids),
                                    uint64_array(entries), len(ids), offset, _stream(device, stream)),
           "restore_blocks")
+
+
+# ---------------------------------------------------------------------------
+# Step inputs: host-to-device uploads read by a kernel
+
+class _PinnedRing:
+    """Pinned host buffers that kvx_upload kernels read, used in turn.
+
+    A buffer is rewritten only after the kernel that last read it has run
+    (an event per buffer; the host waits only if the stream is that far
+    behind). A buffer grows, to a power of two, when an array does not fit.
+    """
+
+    def __init__(self, device: torch.device, count: int = 16):
+        self.device = device
+        self.buffers: list[torch.Tensor | None] = [None] * count
+        self.events: list[torch.cuda.Event | None] = [None] * count
+        self.next = 0
+
+    def stage(self, host: np.ndarray) -> tuple[torch.Tensor, int]:
+        """(a pinned uint8 buffer holding `host`'s bytes, its slot); pass the slot to read_by after the launch."""
+        i = self.next
+        self.next = (i + 1) % len(self.buffers)
+        if self.events[i] is not None:
+            self.events[i].synchronize()
+        nbytes = host.nbytes
+        buf = self.buffers[i]
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(max(256, 1 << (nbytes - 1).bit_length()), dtype=torch.uint8, pin_memory=True)
+            self.buffers[i] = buf
+        buf[:nbytes].numpy()[:] = host.reshape(-1).view(np.uint8)
+        return buf, i
+
+    def read_by(self, i: int, stream: torch.cuda.Stream):
+        event = self.events[i] or torch.cuda.Event()
+        event.record(stream)
+        self.events[i] = event
+
+
+_rings: dict[int, _PinnedRing] = {}
+_rings_lock = threading.Lock()
+
+
+def upload(values: np.ndarray, device: torch.device, stream=None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """A device copy of a host array, read from pinned memory by a kernel on the current stream (kvx_upload).
+
+    Replaces the pinned non-blocking copies of a step's inputs
+    (nanovllm/engine/model_runner.py:169-173, 187-190): a DMA copy on the
+    compute stream queues behind every host-to-device DMA already queued on
+    the device, a restore stream's included, while the kernel does not. The
+    host does not wait for the GPU, except when 16 uploads are still queued.
+    `out` (a contiguous device tensor of the array's dtype and size, e.g. a
+    captured graph's static input) receives the copy instead of a new tensor.
+    """
+    host = np.ascontiguousarray(values)
+    device = torch.device(device)
+    if device.type != "cuda":
+        raise ValueError(f"upload needs a ROCm device (got {device})")
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    device = torch.device("cuda", index)
+    dtype = torch.from_numpy(host[:0]).dtype
+    if out is None:
+        out = torch.empty(host.shape, dtype=dtype, device=device)
+    elif out.device != device or out.dtype != dtype or out.numel() != host.size or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous {dtype} tensor of {host.size} elements on {device}")
+    if host.nbytes == 0:
+        return out
+    if host.nbytes > _lib.UPLOAD_MAX_BYTES:
+        raise ValueError(f"upload of {host.nbytes} bytes exceeds {_lib.UPLOAD_MAX_BYTES}")
+    with _rings_lock:
+        ring = _rings.get(index)
+        if ring is None:
+            ring = _rings[index] = _PinnedRing(device)
+        buf, slot = ring.stage(host)
+        s = torch.cuda.current_stream(device) if stream is None else stream
+        check(lib().kvx_upload(out.data_ptr(), buf.data_ptr(), host.nbytes, _stream(device, s)), "upload")
+        ring.read_by(slot, s)
+    return out
 
 
 # ---------------------------------------------------------------------------

@@ -693,6 +693,56 @@ def test_split_streams_refuse_overlapping_staging(gpu):
         engine.close()
 
 
+def test_replacing_split_staging_orders_both_copy_streams(gpu):
+    """New staging areas on a split-stream cache: each copy stream waits for the other's queued work, so an
+    area one stream still uses can become the other's. Unchanged areas queue no wait."""
+    from kvx.engine.cpu_prefix_cache import _CopyEngine
+
+    pool = torch.zeros((2, 2, 4, BS, 8, 128), dtype=torch.bfloat16, device=gpu)
+    engine = _CopyEngine(pool, ops.pool_layout(pool, torch.float32), ops.FORMAT_FP8, split=True)
+    try:
+        a, b = (torch.empty(engine.entry_stride, dtype=torch.uint8, device=gpu) for _ in range(2))
+        engine.set_staging(a, b, 1)
+        waits = engine.counters()["stream_waits"]
+        engine.set_staging(a, b, 1)
+        assert engine.counters()["stream_waits"] == waits
+        for stream in (engine.save_stream, engine.restore_stream):
+            ops.sleep(20_000, stream=stream, device=gpu)
+        engine.set_staging(b, a, 1)  # swapped while both streams have work queued
+        assert engine.counters()["stream_waits"] == waits + 2
+        engine.synchronize()
+    finally:
+        engine.close()
+
+
+def test_copy_streams_that_cannot_run_side_by_side_warn_and_still_copy(gpu, monkeypatch):
+    from kvx.engine import cpu_prefix_cache
+
+    monkeypatch.setattr(cpu_prefix_cache, "_run_side_by_side", lambda a, b, device: False)
+    pool = make_pool(gpu, 4)
+    manager = BlockManager(4, BS)
+    keys = [publish(manager, b, 40 + b) for b in (0, 1, 2)]
+    expected = {k: block_bytes(pool, b) for k, b in zip(keys, (0, 1, 2))}
+    with pytest.warns(RuntimeWarning, match="serialise"):
+        cache = new_cache(pool, manager, blocks=3, split_streams=True)
+    assert not cache.streams_concurrent and cache.copy_stats["streams_concurrent"] is False
+    for k in keys:
+        assert cache.save_block(k)
+    cache.synchronize()
+    for k in keys:
+        manager.hash_to_block_id.pop(k)
+    pool.fill_(0)
+    with cache.coalesce():  # three restores in one engine call: staged, one DMA
+        targets = {k: cache.restore_block(k) for k in keys}
+    for k in keys:
+        assert np.array_equal(block_bytes(pool, targets[k]), expected[k])
+    stats = cache.copy_stats
+    assert stats["d2h_copies"] >= 1 and stats["d2h_bytes"] >= 3 * cache.block_bytes
+    assert stats["h2d_copies"] >= 1 and stats["h2d_bytes"] >= 3 * cache.block_bytes
+    assert cache.stats == {"saved_blocks": 3, "restored_blocks": 3, "budget_skips": 0}
+    cache.close()
+
+
 def test_a_failed_batch_withdraws_the_metadata_it_published(gpu, monkeypatch):
     pool = make_pool(gpu, 6)
     manager = BlockManager(6, BS)

@@ -5,10 +5,16 @@ Two copy engines share one pool: one stages through attached device buffers
 (kvx_cache_save_noalloc). Both save the same blocks into their own poisoned
 pinned slabs, in two calls in a row, the second with fewer blocks and a
 refilled pool; every payload and scale byte must agree. A call beyond the
-static array's capacity must fail before queuing anything.
+static array's capacity must fail before queuing anything. Allocation-free
+saves of two caches with different save streams, alternating, each hold
+their own blocks' bytes (the array is ordered per device), and a plain C
+program that interposes the HIP runtime's allocation and creation calls sees
+none of them during such saves.
 """
 
 import ctypes
+import subprocess
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -126,3 +132,56 @@ def test_noalloc_save_rejects_more_blocks_than_its_static_staging_holds(gpu):
         assert counters[0].value == 0
     finally:
         engine.close()
+
+
+def test_noalloc_saves_of_two_caches_interleaved_hold_their_own_bytes(gpu):
+    """Each static engine's save stream differs: without the per-device order, one engine's kernel would
+    overwrite the array while the other's copies out of it are still queued."""
+    pool = torch.empty((2, 36, 8, 256, 8, 128), dtype=torch.bfloat16, device=gpu)
+    fill(pool, 11)
+    layout = ops.pool_layout(pool, torch.float32)
+    slots = 6
+    staged = Engine(pool, layout, ops.FORMAT_FP8, slots, staged=True)
+    statics = [Engine(pool, layout, ops.FORMAT_FP8, slots, staged=False) for _ in range(2)]
+    try:
+        compute = torch.cuda.current_stream(gpu).cuda_stream
+        calls = [([0, 1, 2], [0, 1, 2]), ([3, 4, 5], [0, 1, 2]), ([6, 7, 0], [3, 4, 5]), ([1, 3, 5], [3, 4, 5])]
+        for i, (ids, dest) in enumerate(calls):
+            engine = statics[i % 2]
+            print(f"interleaved noalloc call {i} on engine {i % 2}: blocks {ids} -> slots {dest}", flush=True)
+            check(lib().kvx_cache_save_noalloc(engine.handle, int32_array(ids), int32_array(dest), len(ids),
+                                               compute), "kvx_cache_save_noalloc")
+        # The reference bytes: every block once, through attached staging.
+        want = {}
+        for base in range(0, 8, 4):
+            ids = list(range(base, base + 4))
+            check(lib().kvx_cache_save(staged.handle, int32_array(ids), int32_array(range(4)), 4, compute),
+                  "kvx_cache_save")
+            check(lib().kvx_cache_synchronize(staged.handle), "kvx_cache_synchronize")
+            want.update({b: staged.entry(b - base).copy() for b in ids})
+        for engine in statics:
+            check(lib().kvx_cache_synchronize(engine.handle), "kvx_cache_synchronize")
+        final = [{}, {}]
+        for i, (ids, dest) in enumerate(calls):
+            final[i % 2].update(zip(dest, ids))
+        for e, engine in enumerate(statics):
+            for slot, block in final[e].items():
+                for start, end in data_ranges(layout, ops.FORMAT_FP8, engine):
+                    assert np.array_equal(engine.entry(slot)[start:end], want[block][start:end]), \
+                        f"engine {e} slot {slot} (block {block}) bytes [{start}, {end}) differ"
+    finally:
+        staged.close()
+        for engine in statics:
+            engine.close()
+
+
+NOALLOC_CALLS = Path(__file__).resolve().parent / "c_abi" / "noalloc_calls"
+
+
+def test_noalloc_saves_make_no_allocation_or_creation_call(gpu):
+    assert NOALLOC_CALLS.exists(), "build() compiles tests/c_abi/noalloc_calls.c"
+    print("noalloc_calls 5 400", flush=True)
+    proc = subprocess.run([str(NOALLOC_CALLS), "5", "400"], capture_output=True, text=True, timeout=120)
+    print(proc.stdout, proc.stderr, flush=True)
+    assert proc.returncode == 0, proc.stdout + proc.stderr
+    assert "0 allocation or creation calls" in proc.stdout and "0 mismatches" in proc.stdout

@@ -211,19 +211,27 @@ class AgentPressureResult:
 
 def run_agent_pressure(engine, agents: int = 4, context: int = 32768, turns: int = 12, append: int = 2048,
                        seed: int = 0, verify: bool = True, verify_stride: int = 1,
-                       prefetch_hints: bool = True) -> AgentPressureResult:
+                       hints: str | None = "deferred") -> AgentPressureResult:
     """Multi-turn agents sharing one pool: each turn an agent returns with its whole context plus `append`
     new tokens, evicting others' blocks (saved to the CPU tier) and restoring or prefetching its own.
 
     With verify=True every `verify_stride`-th full block (and the last) of each finished request must hold
     either the exact synthetic KV (GPU hit or recomputed) or its FP8 round trip (restored from an FP8 entry) --
-    a block restored from the wrong slot, or read before its restore finished, matches neither. After each
-    request's first step (or, if that step finished it, after it is checked) the next agent's prefix is hinted
-    with prefetch_prefix, so its restores (H2D) overlap the rest of the current request and the saves (D2H) of
-    the blocks it evicts. Hinting before the current request's admission instead would let the prefetch evict
-    the current agent's own cached blocks (the least recently used ones), which its admission would then
-    restore again.
+    a block restored from the wrong slot, or read before its restore finished, matches neither.
+
+    `hints` says when the next agent's prefix is hinted with prefetch_prefix:
+    - "deferred": right after the current request is added, with defer=True. The engine starts the hint in
+      the step that admits the current request, after its admission and before the model runs, so the next
+      agent's restores (H2D) overlap the current request's compute and the saves (D2H) of the blocks they
+      evict;
+    - "after_first_step": after the request's first step (or, if that step finished it, once it is checked),
+      as a client without deferred hints has to: the restores then start after that step's compute;
+    - None: no hints.
+    A hint started before the current request's admission would let the prefetch evict the current agent's
+    own cached blocks (the least recently used ones), which its admission would then restore again.
     """
+    if hints not in ("deferred", "after_first_step", None):
+        raise ValueError(f"unknown hint mode {hints!r}")
     from kvx import ops
     from kvx.engine.sequence import SamplingParams, Sequence
 
@@ -240,7 +248,10 @@ def run_agent_pressure(engine, agents: int = 4, context: int = 32768, turns: int
         for a in range(agents):
             histories[a] += torch.randint(2, 50000, (append,), generator=g).tolist()
             engine.add_request(histories[a], params)
-            nxt = Sequence(histories[(a + 1) % agents]) if prefetch_hints and agents > 1 else None
+            nxt = Sequence(histories[(a + 1) % agents]) if hints and agents > 1 else None
+            if nxt is not None and hints == "deferred":
+                engine.prefetch_prefix(nxt, defer=True)
+                nxt = None
             while not engine.is_finished():
                 engine.step()
                 if nxt is not None and not engine.is_finished():
