@@ -78,6 +78,8 @@ def parse_args():
     p.add_argument("--skip-store", action="store_true", help="skip the store_kvcache leg")
     p.add_argument("--skip-store-concurrency", action="store_true",
                    help="skip the store_kvcache leg's run beside concurrent FP8 saves")
+    p.add_argument("--skip-store-decode", action="store_true",
+                   help="skip store_kvcache in the decode regime (1-512 tokens per step)")
     p.add_argument("--skip-hybrid", action="store_true", help="skip the hybrid-admission calibration leg")
     p.add_argument("--skip-agents", action="store_true", help="skip the agent-pressure leg")
     p.add_argument("--skip-handoff", action="store_true", help="skip the KV handoff leg")
@@ -234,6 +236,99 @@ def store_leg(torch, ops, pool, reps=5, concurrency=True):
     out["writes_only"] = written
     if concurrency:
         out["with_concurrent_saves"] = store_beside_saves(torch, ops, pool, key, value, lengths, reps)
+    return out
+
+
+def store_decode_leg(torch, ops, pool, batches=(1, 8, 64, 256, 512), reps=100):
+    """store_kvcache in the decode regime: one new token per running request, every layer, per step.
+
+    The reference's decode step calls it once per layer with N = the batch
+    (padded to a captured size), inside a CUDA graph for batches up to 512
+    (model_runner.py:201-262, attention.py:59-63). For each N: the host time
+    of one eager ops.store_kvcache call (all checks and the C call), of the
+    bare C call with its arguments prepared, the device time per step of a
+    HIP graph replaying the step's calls, and the device time per step of
+    the same calls issued eagerly back to back. K is contiguous; V is a
+    strided view of a fused QKV row ((32 + 2H) * hd elements), as in
+    Qwen3-8B; slots are distinct random pool slots.
+    """
+    import ctypes as c
+
+    import numpy as np
+
+    from kvx._lib import lib
+
+    _, layers, nb, bs, heads, hd = pool.shape
+    rng = np.random.default_rng(11)
+    stream = torch.cuda.current_stream(pool.device)
+    out = {"layers": layers, "reps": reps}
+    for n in batches:
+        g = torch.Generator(device=pool.device).manual_seed(n)
+        qkv = torch.randn((n, (32 + 2 * heads) * hd), generator=g, device=pool.device).to(torch.bfloat16)
+        key = qkv[:, 32 * hd:(32 + heads) * hd].view(n, heads, hd)
+        value = qkv[:, (32 + heads) * hd:].view(n, heads, hd)
+        mapping = torch.from_numpy(rng.permutation(nb * bs)[:n].astype(np.int32)).to(pool.device)
+        k_caches = [pool[0, layer] for layer in range(layers)]
+        v_caches = [pool[1, layer] for layer in range(layers)]
+
+        def step():
+            for layer in range(layers):
+                ops.store_kvcache(key, value, k_caches[layer], v_caches[layer], mapping)
+
+        raw_args = [(key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0), k_caches[layer].data_ptr(),
+                     v_caches[layer].data_ptr(), mapping.data_ptr(), n, heads, hd, 2,
+                     k_caches[layer].numel() // (heads * hd), c.c_void_p(stream.cuda_stream))
+                    for layer in range(layers)]
+        fn = lib().kvx_store_kvcache
+
+        def raw_step():
+            for args in raw_args:
+                fn(*args)
+
+        res = {}
+        for name, issue in (("eager_call", step), ("bare_c_call", raw_step)):
+            issue()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                issue()
+            host = time.perf_counter() - t0
+            torch.cuda.synchronize()
+            res[f"{name}_host_us"] = round(1e6 * host / (reps * layers), 2)
+        # Device time per step: the step's calls replayed from a captured graph, and issued eagerly after a
+        # long delay kernel so the queue is full before the device reaches them.
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream(pool.device)
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            step()
+        stream.wait_stream(side)
+        with torch.cuda.graph(graph):
+            step()
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with marked(f"store decode: graph, {n} tokens"):
+            e0.record(stream)
+            for _ in range(reps):
+                graph.replay()
+            e1.record(stream)
+            e1.synchronize()
+        res["graph_step_us"] = round(1000 * e0.elapsed_time(e1) / reps, 2)
+        ops.sleep(20_000, stream=stream, device=pool.device)
+        with marked(f"store decode: eager, {n} tokens"):
+            e0.record(stream)
+            for _ in range(20):
+                step()
+            e1.record(stream)
+            e1.synchronize()
+        res["eager_step_us_queued"] = round(1000 * e0.elapsed_time(e1) / 20, 2)
+        res["device_us_per_call"] = round(res["graph_step_us"] / layers, 3)
+        res["host_over_device"] = round(res["eager_call_host_us"] / res["device_us_per_call"], 2)
+        res["algorithmic_bytes_per_call"] = n * (4 * heads * hd * 2 + 4)
+        del graph
+        out[str(n)] = res
+        log(f"store decode {n} tokens: {json.dumps(res)}")
     return out
 
 
@@ -533,6 +628,7 @@ def agent_leg(torch, pool, scale_dtype, h2d_gbs=None):
             with marked(f"agents: {name}"):
                 r = run_agent_pressure(engine, agents=4, context=32768, turns=turns, append=2048, verify=False,
                                        hints=hints)
+            copy_stats = cache.copy_stats
         finally:
             engine.exit()
         if name == "warm-up":
@@ -541,7 +637,8 @@ def agent_leg(torch, pool, scale_dtype, h2d_gbs=None):
                      "restored_blocks": r.restored_blocks, "prefetched_blocks": r.prefetched_blocks,
                      "d2h_bytes": r.d2h_bytes, "h2d_bytes": r.h2d_bytes, "link_gbs": round(r.link_gbs, 2),
                      "host_blocked_s": round(r.host_blocked_s, 3), "drain_s": round(r.drain_s, 4),
-                     "budget_skips": r.budget_skips, "host_budget_bytes": max_bytes, "hints": hints}
+                     "budget_skips": r.budget_skips, "host_budget_bytes": max_bytes, "hints": hints,
+                     "dma_copies": {k: copy_stats[k] for k in ("d2h_copies", "h2d_copies")}}
         if h2d_gbs:
             floor = r.h2d_bytes / (h2d_gbs * 1e9)
             out[name].update(h2d_floor_s=round(floor, 3), wall_over_h2d_floor=round(r.wall_s / floor, 3))
@@ -747,8 +844,10 @@ def handoff_leg(torch, pool, reps=3):
 
 
 def bf16_leg(torch, ops, pool, reps, link=True):
-    """BF16 storage mode on the Qwen3-8B pool: byte gather of 200 seeded blocks into entries and scatter into a
-    seeded permutation of the pool (HBM-resident), then 128 + 128 blocks over the host link."""
+    """BF16 storage mode on the Qwen3-8B pool: byte gather of 200 seeded blocks into entries and scatter into
+    200 other seeded blocks (HBM-resident), then the same 200 blocks over the host link: saved to pinned host
+    slots and restored into those 200 destinations, which overlap the sources (restores into a block being
+    saved wait for its save kernel)."""
     from workloads import block_selection
 
     nb = pool.shape[2]
@@ -762,15 +861,14 @@ def bf16_leg(torch, ops, pool, reps, link=True):
                                      lambda: ops.restore_blocks(pool, dests, entries, ops.FORMAT_RAW))
     del staging
     moved = len(sources) * 2 * BF16_BLOCK_BYTES  # read + written per launch
-    order = block_selection(nb, 256, seed=1)
-    link = host_link_leg(torch, pool, layout, order[:128], order[128:], reps, fmt=ops.FORMAT_RAW,
+    link = host_link_leg(torch, pool, layout, sources, dests, reps, fmt=ops.FORMAT_RAW,
                          ceilings=False) if link else None
     return {"blocks": len(sources), "algorithmic_bytes_per_launch": moved,
             "gather": {"ms": round(1000 * gather_s, 4), "hbm_gbs": round(moved / gather_s / 1e9, 1),
                        "frac": round(moved / gather_s / 1e9 / HBM_PEAK_GBS, 4)},
             "scatter": {"ms": round(1000 * scatter_s, 4), "hbm_gbs": round(moved / scatter_s / 1e9, 1),
                         "frac": round(moved / scatter_s / 1e9 / HBM_PEAK_GBS, 4)},
-            "host_link_128_blocks": link}
+            "host_link_200_blocks": link}
 
 
 def qwen3_0_6b_leg(torch, ops, scale_dtype):
@@ -816,9 +914,13 @@ def host_link_leg(torch, pool, layout, sources, dests, reps, fmt=None, ceilings=
         engine.set_staging(save_staging, restore_staging, n)
         compute = torch.cuda.current_stream(pool.device).cuda_stream
         low, high = list(range(n)), list(range(n, 2 * n))
+        # DMA copies queued per phase (the engine's counters, or the pieces a memcpy phase queues): a memory-copy
+        # trace of the phase must hold exactly this many records per direction.
+        copies = {}
 
-        def timed(fn, label="host link"):
+        def timed(fn, label="host link", pieces_per_rep=None):
             best = None
+            before = engine.dma_counters()
             with marked(label):
                 for _ in range(reps):
                     torch.cuda.synchronize()
@@ -828,6 +930,11 @@ def host_link_leg(torch, pool, layout, sources, dests, reps, fmt=None, ceilings=
                     torch.cuda.synchronize()
                     dt = time.perf_counter() - t0
                     best = dt if best is None else min(best, dt)
+            after = engine.dma_counters()
+            copies[label] = {k: after[k] - before[k] for k in ("d2h_copies", "h2d_copies")}
+            if pieces_per_rep:
+                for k, v in pieces_per_rep.items():
+                    copies[label][k] += reps * v
             return best
 
         engine.save(sources, low, compute)  # fill the restore source slots
@@ -922,9 +1029,13 @@ def host_link_leg(torch, pool, layout, sources, dests, reps, fmt=None, ceilings=
                     assert hip.hipMemcpyAsync(flat_dev2.data_ptr() + off, host_b + off, size, 1, s2) == 0
 
             piece_sizes = (8 << 20, 16 << 20, 32 << 20, 64 << 20, -(-link_bytes // 16))
-            ceil_d2h = min(timed(lambda: d2h(p), f"memcpy d2h, {p} B pieces") for p in piece_sizes)
-            ceil_h2d = min(timed(lambda: h2d(p), f"memcpy h2d, {p} B pieces") for p in piece_sizes)
-            ceil_both = min(timed(lambda: both_ways(p), f"memcpy both, {p} B pieces") for p in piece_sizes)
+            ceil_d2h = min(timed(lambda: d2h(p), f"memcpy d2h, {p} B pieces", {"d2h_copies": len(pieces(p))})
+                           for p in piece_sizes)
+            ceil_h2d = min(timed(lambda: h2d(p), f"memcpy h2d, {p} B pieces", {"h2d_copies": len(pieces(p))})
+                           for p in piece_sizes)
+            ceil_both = min(timed(lambda: both_ways(p), f"memcpy both, {p} B pieces",
+                                  {"d2h_copies": len(pieces(p)), "h2d_copies": len(pieces(p))})
+                            for p in piece_sizes)
         overlap = (save_s + restore_s - both_s) / min(save_s, restore_s)
         duplex = gbs(2 * link_bytes, both_s)
         out = {
@@ -941,6 +1052,7 @@ def host_link_leg(torch, pool, layout, sources, dests, reps, fmt=None, ceilings=
             "streams_concurrent": engine.streams_concurrent,
             "per_block_calls": per_block,
             "calls_of_4_blocks": per_4_blocks,
+            "dma_copies_by_phase": copies,
         }
         if ceilings:
             out.update({
@@ -984,6 +1096,71 @@ def pcie_path(bdf):
     return hops
 
 
+def _cpu_list(text):
+    """CPU ids of a sysfs cpulist ("0-3,8,10-11")."""
+    cpus = set()
+    for part in text.strip().split(","):
+        if part:
+            lo, _, hi = part.partition("-")
+            cpus.update(range(int(lo), int(hi or lo) + 1))
+    return cpus
+
+
+def pages_by_node(address, maps_path="/proc/self/maps", numa_maps_path="/proc/self/numa_maps"):
+    """{node: pages} of the mapping that holds `address`, from numa_maps (None if not found)."""
+    try:
+        start = None
+        with open(maps_path) as maps:
+            for line in maps:
+                lo, hi = (int(x, 16) for x in line.split()[0].split("-"))
+                if lo <= address < hi:
+                    start = lo
+                    break
+        if start is None:
+            return None
+        with open(numa_maps_path) as numa:
+            for line in numa:
+                fields = line.split()
+                if int(fields[0], 16) == start:
+                    return {f[1:f.index("=")]: int(f[f.index("=") + 1:]) for f in fields
+                            if f[0] == "N" and "=" in f and f[1:f.index("=")].isdigit()}
+    except (OSError, ValueError):
+        return None
+    return None
+
+
+def numa_placement(torch, bdf, sysfs="/sys"):
+    """Where the host link's ends sit: the GPU's NUMA node (its PCI function), the nodes of the CPUs this
+    process may run on, and the nodes holding the pages of a fresh pinned allocation (as the cache's slabs are
+    made). -1 or None where the kernel does not say."""
+    out = {"nodes": {}, "gpu_numa_node": None, "affinity_cpus_by_node": {}, "pinned_pages_by_node": None}
+    try:
+        node_dirs = sorted(p for p in Path(sysfs, "devices/system/node").glob("node[0-9]*"))
+    except OSError:
+        node_dirs = []
+    affinity = os.sched_getaffinity(0)
+    for d in node_dirs:
+        try:
+            cpus = _cpu_list(Path(d, "cpulist").read_text())
+        except OSError:
+            continue
+        node = d.name[4:]
+        out["nodes"][node] = len(cpus)
+        mine = sorted(cpus & affinity)
+        if mine:
+            out["affinity_cpus_by_node"][node] = len(mine)
+    if bdf:
+        try:
+            out["gpu_numa_node"] = int(Path(sysfs, "bus/pci/devices", bdf, "numa_node").read_text())
+        except (OSError, ValueError):
+            pass
+    if torch is not None:
+        probe = torch.ones(64 << 20, dtype=torch.uint8, pin_memory=True)
+        out["pinned_pages_by_node"] = pages_by_node(probe.data_ptr())
+        del probe
+    return out
+
+
 def host_inventory(torch):
     """What the CPU baseline and the host link run on (the reference records the same: bench/inventory.py:79-105)."""
     affinity = len(os.sched_getaffinity(0))
@@ -1019,7 +1196,7 @@ def host_inventory(torch):
             "lscpu_sockets": lscpu.get("Socket(s)"),
             "usable_cpus": usable, "torch_threads_default": torch.get_num_threads(),
             "omp_num_threads": os.environ.get("OMP_NUM_THREADS"), "gpu": torch.cuda.get_device_name(0),
-            "gpu_pci": bdf, "pcie_path": pcie_path(bdf)}
+            "gpu_pci": bdf, "pcie_path": pcie_path(bdf), "numa": numa_placement(torch, bdf)}
 
 
 def headline_leg(torch, pool, layout, sources, dests, steps, warmup):
@@ -1335,7 +1512,7 @@ def interference_leg(torch, nbytes=1 << 30, reps=20, kvx_kernels=None):
     return out
 
 
-def cpu_baseline_leg(torch, pool, sources, dests, scale_dtype, inventory, pairs=48, runs=5):
+def cpu_baseline_leg(torch, pool, sources, dests, scale_dtype, inventory, pairs=128, runs=5):
     """The reference's CPU path on this host: its torch codec and byte copies on CPU tensors, the branches
     CPUBlockCache takes for a CPU pool (cpu_prefix_cache.py:20-28, 323-326, 394-397).
 
@@ -1343,9 +1520,14 @@ def cpu_baseline_leg(torch, pool, sources, dests, scale_dtype, inventory, pairs=
     cgroup quota). Each measurement is 1 warm-up and the median of `runs`
     runs (time.perf_counter). Samples: `pairs` of the Qwen3-8B workload's
     Student-t blocks (copied from the GPU pool) saved to FP8 and restored into
-    other blocks, the same `pairs` in BF16 mode, and config 1's 16 Qwen3-0.6B
-    N(0, 1) blocks.
+    other blocks, the same `pairs` in BF16 mode, and config 1 as written: 16
+    N(0, 1) blocks of a 512-block Qwen3-0.6B host pool saved and restored into
+    16 other seeded blocks. Only the blocks the workload touches are written;
+    the rest of the 15 GB pool is allocated but never touched, so its pages
+    are not materialised.
     """
+    from workloads import QWEN3_0_6B, block_selection
+
     from oracle import torch_path
 
     threads = inventory["usable_cpus"]
@@ -1361,30 +1543,35 @@ def cpu_baseline_leg(torch, pool, sources, dests, scale_dtype, inventory, pairs=
             times.append(time.perf_counter() - t0)
         return sorted(times)[runs // 2]
 
-    def codec(host, n, fmt_scale):
-        entry = (n, 2, host.shape[1], *host.shape[3:])
+    def codec(host, src, dst, fmt_scale):
+        entry = (len(src), 2, host.shape[1], *host.shape[3:])
         payload = torch.empty(entry, dtype=torch.float8_e4m3fn if fmt_scale else host.dtype)
         scale = torch.empty((*entry[:-1], 1), dtype=fmt_scale) if fmt_scale else None
 
         def save():
-            for i in range(n):
-                torch_path.save_block(host, i, payload[i], None if scale is None else scale[i])
+            for i, b in enumerate(src):
+                torch_path.save_block(host, b, payload[i], None if scale is None else scale[i])
 
         def restore():
-            for i in range(n):
-                torch_path.restore_block(host, n + i, payload[i], None if scale is None else scale[i])
+            for i, b in enumerate(dst):
+                torch_path.restore_block(host, b, payload[i], None if scale is None else scale[i])
 
         return median_s(save), median_s(restore)
 
     host = torch.empty((2, layers, 2 * pairs, bs, heads, hd), dtype=pool.dtype)
     host[:, :, :pairs] = pool[:, :, sources[:pairs]].cpu()
-    fp8_save, fp8_restore = codec(host, pairs, scale_dtype)
-    raw_save, raw_restore = codec(host, pairs, None)
+    src, dst = list(range(pairs)), list(range(pairs, 2 * pairs))
+    fp8_save, fp8_restore = codec(host, src, dst, scale_dtype)
+    raw_save, raw_restore = codec(host, src, dst, None)
     del host
-    small = torch.randn((2, 28, 32, 256, 8, 128), generator=torch.Generator(device="cuda").manual_seed(0),
-                        device="cuda").to(torch.bfloat16).cpu()
-    c1_save, c1_restore = codec(small, 16, torch.float32)
+    small = torch.empty(QWEN3_0_6B.shape, dtype=torch.bfloat16)
+    order = block_selection(QWEN3_0_6B.num_blocks, 32, seed=1)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    for b in order:
+        small[:, :, b] = torch.randn(small[:, :, b].shape, generator=g, device="cuda").to(torch.bfloat16).cpu()
+    c1_save, c1_restore = codec(small, order[:16], order[16:], torch.float32)
     small_block = small[:, :, 0].numel() * 2
+    del small
     logical = lambda n, per, s: round(n * per / s / 1e9, 3)  # noqa: E731
     value = logical(2 * pairs, BF16_BLOCK_BYTES, fp8_save + fp8_restore)
     return {
@@ -1401,7 +1588,8 @@ def cpu_baseline_leg(torch, pool, sources, dests, scale_dtype, inventory, pairs=
         "bf16_qwen3_8b": {"blocks": pairs, "save_s": round(raw_save, 4), "restore_s": round(raw_restore, 4),
                           "save_gbs": logical(pairs, BF16_BLOCK_BYTES, raw_save),
                           "restore_gbs": logical(pairs, BF16_BLOCK_BYTES, raw_restore)},
-        "fp8_qwen3_0_6b_16_blocks": {"save_s": round(c1_save, 4), "restore_s": round(c1_restore, 4),
+        "fp8_qwen3_0_6b_16_blocks": {"pool": list(QWEN3_0_6B.shape), "save_s": round(c1_save, 4),
+                                     "restore_s": round(c1_restore, 4),
                                      "logical_kv_gbs": logical(32, small_block, c1_save + c1_restore)},
         "threads_basis": "sched_getaffinity capped by the cgroup CPU quota",
         "torch_threads": torch.get_num_threads(),
@@ -1523,6 +1711,9 @@ def main():
     if not args.skip_store:
         log("store_kvcache leg")
         result["store_kvcache"] = store_leg(torch, ops, pool, concurrency=not args.skip_store_concurrency)
+    if not args.skip_store_decode:
+        log("store_kvcache decode leg")
+        result["store_kvcache_decode"] = store_decode_leg(torch, ops, pool)
     if args.calibrate_copy:
         raw_layout = ops.pool_layout(pool)
         _, _, raw_stride = ops.entry_layout(raw_layout, ops.FORMAT_RAW)

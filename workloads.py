@@ -305,3 +305,4 @@ def run_agent_pressure(engine, agents: int = 4, context: int = 32768, turns: int
                                cache.prefetched_blocks if cache is not None else 0, stats["budget_skips"],
                                stats["saved_blocks"] * entry, stats["restored_blocks"] * entry, checked, fp8_hits,
                                blocked, drain)
+
