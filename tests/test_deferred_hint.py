@@ -13,8 +13,8 @@ import pytest
 
 from kvx.engine.llm_engine import LLMEngine
 from kvx.engine.scheduler import Scheduler
-from kvx.engine.sequence import Sequence
-from test_block_manager import BS, RecordingCache, consistent, cpu_only_prefix, params
+from kvx.engine.sequence import SamplingParams, Sequence
+from test_block_manager import BS, Entry, RecordingCache, consistent, cpu_only_prefix, params
 
 
 def scheduler(num_blocks, budget=4096):
@@ -125,3 +125,45 @@ def test_engine_keeps_a_deferred_hint_and_drops_an_immediate_one():
     engine.scheduler.block_manager._last_prefetch = None
     assert engine.prefetch_prefix(hint, defer=True) == 0  # both CPU hits are now idle GPU hits
     consistent(engine.scheduler.block_manager)
+
+
+def test_seeded_streams_with_deferred_hints_keep_the_pool_consistent():
+    """Random arrivals, decode lengths and hints, deferred or not, through the real scheduler: after every step
+    the free order and the references agree, every block in a table is referenced once per table, and a pass that
+    started the kept hint left no request waiting without blocks."""
+    import random
+
+    for seed in range(40):
+        rng = random.Random(seed)
+        sched, cache = scheduler(rng.randint(6, 12), budget=rng.choice([256, 512, 2048]))
+        manager = sched.block_manager
+        docs = [[100 * d + i for i in range(rng.randint(1, 4))] for d in range(4)]
+        for d, doc in enumerate(docs[:2]):  # some documents start as CPU-only prefixes
+            h = -1
+            for i, token in enumerate(doc):
+                h = manager.compute_hash([token] * BS, h)
+                cache.entries[h] = Entry(tuple([token] * BS), slot=10 * d + i)
+        for step in range(50):
+            for _ in range(rng.choice([0, 0, 1, 2])):
+                doc = rng.choice(docs)
+                tokens = [v for v in doc[:rng.randint(1, len(doc))] for _ in range(BS)] + [7] * rng.randint(1, 50)
+                if len(tokens) // BS + 2 < len(manager.blocks):
+                    sched.add(Sequence(tokens, SamplingParams(temperature=0, max_tokens=rng.randint(1, 4),
+                                                              ignore_eos=True)))
+            if rng.random() < 0.4:
+                hint = rng.choice(docs)
+                sched.prefetch_hint = Sequence([v for v in hint for _ in range(BS)] + [1], params())
+            if sched.is_finished():
+                continue
+            hint = sched.prefetch_hint
+            seqs, is_prefill = sched.schedule()
+            if hint is not None and sched.prefetch_hint is None:  # the pass started the kept hint
+                assert all(s.block_table for s in sched.waiting), (seed, step)
+            sched.postprocess(seqs, [7] * len(seqs), is_prefill)
+            consistent(manager)
+            refs = {}
+            for s in list(sched.running) + list(sched.waiting):
+                for b in s.block_table:
+                    refs[b] = refs.get(b, 0) + 1
+            for b, n in refs.items():
+                assert manager.blocks[b].ref_count == n, (seed, step, b)

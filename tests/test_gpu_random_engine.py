@@ -3,7 +3,8 @@
 LLMEngine with the synthetic KV runner (store_kvcache writes K/V that are a function of each token and its
 position) and a real CPUBlockCache on libkvx: requests drawn from documents that share leading blocks arrive at
 random steps, so admissions hit GPU blocks, restore CPU entries (waited, split or prefetched), recycle and save
-victims, and decode into fresh blocks. When a request finishes, each of its published full blocks must hold
+victims, and decode into fresh blocks; hints are started at once or, deferred, after a step's admissions. When a
+request finishes, each of its published full blocks must hold
 exactly the KV its tokens and positions define, or that KV's FP8 round trip when the block came back from an
 FP8 entry. A restore from the wrong slot, a block read before its restore landed or overwritten before its save
 read it, shows up as neither.
@@ -78,7 +79,12 @@ def run_stream(gpu, seed, fp8, split, batched, options, monkeypatch, heads=2, he
                                                                    ignore_eos=True))
                 prompts[seq_id] = tokens
                 if options.get("prefetch") and rng.random() < 0.3:
-                    engine.prefetch_prefix(tokens)
+                    if options.get("defer_hints"):
+                        # A likely later request: the engine starts it after this step's admissions.
+                        hint = rng.choice(documents)
+                        engine.prefetch_prefix([v for v in hint for _ in range(BS)] + [1], defer=True)
+                    else:
+                        engine.prefetch_prefix(tokens)
             if engine.is_finished():
                 continue
             finished, _ = engine.step()
@@ -97,7 +103,7 @@ def run_stream(gpu, seed, fp8, split, batched, options, monkeypatch, heads=2, he
                     assert kind, (f"seed {seed} step {step}: block {i} of request {seq_id} (GPU block {block_id}) "
                                   "holds neither its KV nor the FP8 round trip of it")
                     counts[kind] += 1
-        stats = cache.stats
+        stats = dict(cache.stats, prefetched_blocks=cache.prefetched_blocks)
     finally:
         engine.exit()
     return counts, stats
@@ -105,6 +111,7 @@ def run_stream(gpu, seed, fp8, split, batched, options, monkeypatch, heads=2, he
 
 OPTIONS = [pytest.param({}, id="plain"), pytest.param({"prefetch": True, "save_on_release": True}, id="prefetch"),
            pytest.param({"eviction": "mru", "prefetch": True}, id="mru"),
+           pytest.param({"prefetch": True, "defer_hints": True, "save_on_release": True}, id="deferred"),
            pytest.param({"hybrid": (2e-4, 1e-6, 0.0), "save_on_release": True}, id="hybrid")]
 
 
@@ -112,15 +119,18 @@ OPTIONS = [pytest.param({}, id="plain"), pytest.param({"prefetch": True, "save_o
 @pytest.mark.parametrize("fp8,split,batched", [(True, True, True), (True, False, False), (False, True, False),
                                                (False, False, True)])
 def test_random_request_streams_keep_every_block_intact(gpu, fp8, split, batched, options, monkeypatch):
-    totals = {"exact": 0, "fp8": 0, "requests": 0, "restored": 0, "saved": 0}
+    totals = {"exact": 0, "fp8": 0, "requests": 0, "restored": 0, "saved": 0, "prefetched": 0}
     for seed in range(8):
         counts, stats = run_stream(gpu, seed, fp8, split, batched, options, monkeypatch)
         for key in ("exact", "fp8", "requests"):
             totals[key] += counts[key]
         totals["restored"] += stats["restored_blocks"]
         totals["saved"] += stats["saved_blocks"]
+        totals["prefetched"] += stats["prefetched_blocks"]
     print(totals)
     assert totals["requests"] > 0 and totals["saved"] > 0 and totals["restored"] > 0
+    if options.get("defer_hints"):
+        assert totals["prefetched"] > 0  # deferred hints started after admissions
     if fp8:
         assert totals["fp8"] > 0  # some verified blocks came back from FP8 entries
 
