@@ -72,8 +72,8 @@ def parse_args():
     p.add_argument("--scale", choices=("fp32", "bf16"), default="fp32")
     p.add_argument("--skip-host-link", action="store_true")
     p.add_argument("--skip-sdma-probe", action="store_true",
-                   help="skip the host-link probe that queues HSA copies on explicit SDMA engines (it crashed the "
-                        "process under rocprofv3's memory-copy tracing, which intercepts those calls)")
+                   help="skip the host-link probe that queues HSA copies on explicit SDMA engines (it also skips "
+                        "itself when a profiler tool is loaded)")
     p.add_argument("--skip-cpu-baseline", action="store_true")
     p.add_argument("--skip-store", action="store_true", help="skip the store_kvcache leg")
     p.add_argument("--skip-store-concurrency", action="store_true",

@@ -242,8 +242,7 @@ class _PinnedRing:
     behind). A buffer grows, to a power of two, when an array does not fit.
     """
 
-    def __init__(self, device: torch.device, count: int = 16):
-        self.device = device
+    def __init__(self, count: int = 16):
         self.buffers: list[torch.Tensor | None] = [None] * count
         self.events: list[torch.cuda.Event | None] = [None] * count
         self.next = 0
@@ -301,7 +300,7 @@ def upload(values: np.ndarray, device: torch.device, stream=None, out: torch.Ten
     with _rings_lock:
         ring = _rings.get(index)
         if ring is None:
-            ring = _rings[index] = _PinnedRing(device)
+            ring = _rings[index] = _PinnedRing()
         buf, slot = ring.stage(host)
         s = torch.cuda.current_stream(device) if stream is None else stream
         check(lib().kvx_upload(out.data_ptr(), buf.data_ptr(), host.nbytes, _stream(device, s)), "upload")

@@ -110,3 +110,22 @@ def test_upload_does_not_wait_for_dma_queued_on_another_stream(gpu):
     dma_ms, upload_ms = start.elapsed_time(dma_done), start.elapsed_time(upload_done)
     print(f"1 GiB H2D DMA {dma_ms:.2f} ms; 256 KiB upload done at {upload_ms:.2f} ms", flush=True)
     assert upload_ms < dma_ms / 2
+
+
+def test_a_captured_upload_reads_the_pinned_source_at_each_replay(gpu):
+    """A graph holding kvx_upload (as a decode graph would hold its static inputs' copies): the host rewrites the
+    pinned source between replays, with eager work in between, and every replay lands the current contents."""
+    src = torch.zeros(4096, dtype=torch.int32).pin_memory()
+    dst = torch.full((4096,), -1, dtype=torch.int32, device=gpu)
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize(gpu)
+    with torch.cuda.graph(graph):
+        stream = torch.cuda.current_stream(gpu).cuda_stream
+        check(lib().kvx_upload(dst.data_ptr(), src.data_ptr(), src.numel() * 4, stream), "upload")
+    scratch = torch.empty(1 << 20, device=gpu)
+    for replay in range(5):
+        src.copy_(torch.arange(4096, dtype=torch.int32) * (replay + 3))
+        graph.replay()
+        scratch.mul_(2).add_(1)  # eager work between replays
+        torch.cuda.synchronize(gpu)
+        assert torch.equal(dst.cpu(), src), f"replay {replay}"
