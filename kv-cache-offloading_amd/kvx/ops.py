@@ -281,6 +281,7 @@ def upload(values: np.ndarray, device: torch.device, stream=None, out: torch.Ten
     host does not wait for the GPU, except when 16 uploads are still queued.
     `out` (a contiguous device tensor of the array's dtype and size, e.g. a
     captured graph's static input) receives the copy instead of a new tensor.
+    `stream` is a torch.cuda.Stream of the device (default: its current stream).
     """
     host = np.ascontiguousarray(values)
     device = torch.device(device)
@@ -297,6 +298,8 @@ def upload(values: np.ndarray, device: torch.device, stream=None, out: torch.Ten
         return out
     if host.nbytes > _lib.UPLOAD_MAX_BYTES:
         raise ValueError(f"upload of {host.nbytes} bytes exceeds {_lib.UPLOAD_MAX_BYTES}")
+    if stream is not None and not isinstance(stream, torch.cuda.Stream):
+        raise TypeError("stream must be a torch.cuda.Stream")
     with _rings_lock:
         ring = _rings.get(index)
         if ring is None:
