@@ -259,3 +259,17 @@ def test_spans_beyond_two_to_the_40_bytes_are_refused_before_any_device_work():
     with pytest.raises(NotImplementedError, match="2\\^40"):
         _lib.check(handle.kvx_restore_blocks(4096, ctypes.byref(wide), ops.FORMAT_FP8, table,
                                              _lib.uint64_array([4096]), 1, 0, None))
+
+
+def test_upload_and_dma_counters_reject_bad_arguments_before_any_device_work():
+    handle = _lib.lib()
+    with pytest.raises(ValueError, match="negative byte count"):
+        _lib.check(handle.kvx_upload(16, 16, -1, None))
+    with pytest.raises(IndexError, match="largest upload"):
+        _lib.check(handle.kvx_upload(16, 16, _lib.UPLOAD_MAX_BYTES + 1, None))
+    with pytest.raises(ValueError, match="NULL"):
+        _lib.check(handle.kvx_upload(0, 16, 64, None))
+    _lib.check(handle.kvx_upload(0, 0, 0, None))  # nothing to copy: no pointer is looked at
+    counts = [ctypes.c_int64() for _ in range(4)]
+    with pytest.raises(ValueError, match="NULL cache"):
+        _lib.check(handle.kvx_cache_dma_counters(None, *map(ctypes.byref, counts)))
