@@ -100,6 +100,37 @@ def test_chained_hashes_depend_on_the_prefix():
     assert BlockManager.compute_hash([2] * BS, a) != BlockManager.compute_hash([2] * BS)
 
 
+def test_block_hash_known_answers_and_the_reference_construction():
+    """block_manager.py:67-73 streams the 8-byte prefix and np.array(token_ids).tobytes() into xxh64; the engine
+    packs the int64 tokens with struct in one buffer. Golden values, then agreement on random blocks."""
+    import random
+
+    import numpy as np
+    import xxhash
+
+    def streamed(token_ids, prefix=-1):
+        h = xxhash.xxh64()
+        if prefix != -1:
+            h.update(prefix.to_bytes(8, "little"))
+        h.update(np.array(token_ids).tobytes())
+        return h.intdigest()
+
+    a = BlockManager.compute_hash([1] * BS)
+    b = BlockManager.compute_hash(list(range(BS)), a)
+    c = BlockManager.compute_hash([2**63 - 1, -1, 0, 151643], b)
+    assert (a, b, c) == (18283542310692251843, 9163549530594832100, 16783557659952266248)
+    rng = random.Random(3)
+    prefix = -1
+    for n in [BS, BS, 16, 1, 0, 255, 257, BS]:
+        tokens = [rng.choice([rng.randrange(0, 200_000), rng.randrange(-2**63, 2**63)]) for _ in range(n)]
+        got = BlockManager.compute_hash(tokens, prefix)
+        assert got == streamed(tokens, prefix), (n, prefix)
+        prefix = got
+    # Token ids outside int64 are refused (numpy would hash a lone 2**63 as uint64; vocabularies are far smaller).
+    with pytest.raises(Exception):
+        BlockManager.compute_hash([2**63])
+
+
 def test_mru_eviction_recycles_the_latest_release_tail_first():
     # bench/test_cpu_cache_optimizations.py:214-232
     manager = BlockManager(6, BS, "mru")
