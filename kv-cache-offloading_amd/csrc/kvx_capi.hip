@@ -903,7 +903,16 @@ int kvx_cache_create(void* pool, const kvx_block_layout* layout, int32_t format,
   c->pending_restore.assign(layout->num_blocks, nullptr);
   DeviceScope scope;
   rc = scope.enter(device);
-  if (!rc) rc = hip_status(hipEventCreateWithFlags(&c->marker, hipEventDisableTiming), "hipEventCreate");
+  // The marker only orders device work behind device work: saves behind the
+  // caller's writes of their pool blocks, restores behind the caller's reads
+  // of their destinations, and each copy stream behind the other's use of a
+  // re-cut staging area. Hand-offs through host slots wait on the pooled
+  // events, which keep the system-scope release. A device-scope release cut
+  // the host cost of the wait behind a busy stream from 12.6 to 6.6 us on
+  // MI355X.
+  if (!rc)
+    rc = hip_status(hipEventCreateWithFlags(&c->marker, hipEventDisableTiming | hipEventReleaseToDevice),
+                    "hipEventCreate");
   if (!rc) rc = c->new_event(&c->static_done);
   if (rc) {
     kvx_cache_destroy(c);

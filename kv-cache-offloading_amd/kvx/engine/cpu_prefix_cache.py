@@ -445,6 +445,7 @@ class CPUBlockCache:
         self._fp8, self._scale_dtype = fp8, scale_dtype
         self._save_on_release, self._prefetch = save_on_release, prefetch
         self._cache, self._manager = pool, block_manager
+        self._device_index = pool.device.index
         self._shape = (2, pool.shape[1], *pool.shape[3:])  # one block: [K/V, layer, token, KV head, head dim]
         self._max_bytes = max_bytes
         self._layout = ops.pool_layout(pool, scale_dtype if fp8 else None)
@@ -587,7 +588,8 @@ class CPUBlockCache:
         self._staging = [save, restore]
 
     def _compute_stream(self) -> int:
-        return torch.cuda.current_stream(self._cache.device).cuda_stream
+        # The raw handle: building a torch Stream object on every copy call cost a few microseconds each.
+        return torch._C._cuda_getCurrentRawStream(self._device_index)
 
     def _save_to_slot(self, block_id: int, slot: int):
         """Queue pool block -> host slot on the save stream (the seam failure-injection tests patch)."""
