@@ -282,6 +282,9 @@ def upload(values: np.ndarray, device: torch.device, stream=None, out: torch.Ten
     `out` (a contiguous device tensor of the array's dtype and size, e.g. a
     captured graph's static input) receives the copy instead of a new tensor.
     `stream` is a torch.cuda.Stream of the device (default: its current stream).
+    Eager only: later uploads rewrite the ring's buffers, so a captured graph
+    would replay whatever they hold by then. Inside a graph, call kvx_upload
+    with a pinned source the caller owns and rewrites between replays.
     """
     host = np.ascontiguousarray(values)
     device = torch.device(device)
