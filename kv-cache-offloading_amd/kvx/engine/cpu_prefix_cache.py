@@ -170,9 +170,6 @@ class _CopyEngine:
         """Negative controls for tests: drop ordering rules (kvx._lib.DEBUG_*); results become wrong."""
         check(lib().kvx_cache_set_debug(self.handle, flags), "kvx_cache_set_debug")
 
-    def reset_slabs(self):
-        check(lib().kvx_cache_reset_slabs(self.handle), "kvx_cache_reset_slabs")
-
     def close(self):
         if self.handle:
             handle, self.handle = self.handle, None
