@@ -78,6 +78,8 @@ def parse_args():
     p.add_argument("--skip-store", action="store_true", help="skip the store_kvcache leg")
     p.add_argument("--skip-store-concurrency", action="store_true",
                    help="skip the store_kvcache leg's run beside concurrent FP8 saves")
+    p.add_argument("--skip-tp-rank", action="store_true",
+                   help="skip config 2 at one TP=8 rank's share of the pool (1 KV head)")
     p.add_argument("--skip-store-decode", action="store_true",
                    help="skip store_kvcache in the decode regime (1-512 tokens per step)")
     p.add_argument("--skip-hybrid", action="store_true", help="skip the hybrid-admission calibration leg")
@@ -107,8 +109,9 @@ def pmc_traffic(kernel_prefix: str):
     return None, None
 
 
-def kernel_leg(torch, ops, pool, sources, dests, scale_dtype, steps, warmup):
-    """HBM-resident save + restore; returns timings and algorithmic byte counts."""
+def kernel_leg(torch, ops, pool, sources, dests, scale_dtype, steps, warmup, block_bytes=BF16_BLOCK_BYTES,
+               label="kernel leg"):
+    """HBM-resident save + restore; returns timings and algorithmic byte counts (`block_bytes`: one pool block)."""
     layout = ops.pool_layout(pool, scale_dtype)
     logical, offset, stride = ops.entry_layout(layout, ops.FORMAT_FP8)
     n = len(sources)
@@ -131,14 +134,14 @@ def kernel_leg(torch, ops, pool, sources, dests, scale_dtype, steps, warmup):
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    with marked("kernel leg: timed steps"):
+    with marked(f"{label}: timed steps"):
         for ev in events:
             step(ev)
         torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     save_ms = sum(e[0].elapsed_time(e[1]) for e in events) / steps
     restore_ms = sum(e[1].elapsed_time(e[2]) for e in events) / steps
-    hbm_bytes = n * (BF16_BLOCK_BYTES + logical)  # per launch, either direction
+    hbm_bytes = n * (block_bytes + logical)  # per launch, either direction
     return dict(elapsed=elapsed, save_ms=save_ms, restore_ms=restore_ms, hbm_bytes=hbm_bytes,
                 logical_entry=logical, entry_stride=stride)
 
@@ -1199,7 +1202,7 @@ def host_inventory(torch):
             "gpu_pci": bdf, "pcie_path": pcie_path(bdf), "numa": numa_placement(torch, bdf)}
 
 
-def headline_leg(torch, pool, layout, sources, dests, steps, warmup):
+def headline_leg(torch, pool, layout, sources, dests, steps, warmup, label="headline"):
     """Config 2 end to end: each step saves the sources into pinned host slots and restores as many host entries
     into the destinations, overlapped on the copy engine's save and restore streams (the C ABI calls the cache
     makes: one kvx_cache_save and one kvx_cache_restore of 128 blocks)."""
@@ -1227,7 +1230,7 @@ def headline_leg(torch, pool, layout, sources, dests, steps, warmup):
             step()
         engine.synchronize()
         torch.cuda.synchronize()
-        with marked("headline: timed steps"):
+        with marked(f"{label}: timed steps"):
             t0 = time.perf_counter()
             for _ in range(steps):
                 step()
@@ -1238,6 +1241,42 @@ def headline_leg(torch, pool, layout, sources, dests, steps, warmup):
                 "streams_concurrent": engine.streams_concurrent}
     finally:
         engine.close()
+
+
+def tp_rank_leg(torch, ops, scale_dtype, steps, warmup, tp=8, blocks=128):
+    """Config 2 at one tensor-parallel rank's share of the pool.
+
+    Under TP each rank's pool holds num_kv_heads // tp heads (model_runner.py:110): at TP=8 Qwen3-8B's pool is
+    [2, 36, 320, 256, 1, 128] per rank, and each rank saves and restores its head slice of every block over its
+    own host link. Same values, seeds and 128 + 128 blocks as the headline: the FP8 kernels with entries in HBM
+    (per-launch algorithmic bytes as the headline's, for the rank's block), then the overlapped pinned-slab step.
+    """
+    from workloads import PoolShape, block_selection, fill_student_t
+
+    shape = PoolShape(layers=36, num_blocks=320, kv_heads=8 // tp)
+    pool = torch.empty(shape.shape, dtype=torch.bfloat16, device="cuda")
+    fill_student_t(pool, seed=0)
+    order = block_selection(shape.num_blocks, 2 * blocks, seed=1)
+    sources, dests = order[:blocks], order[blocks:]
+    layout = ops.pool_layout(pool, scale_dtype)
+    k = kernel_leg(torch, ops, pool, sources, dests, scale_dtype, steps, warmup, block_bytes=shape.block_bytes_bf16,
+                   label=f"tp{tp} rank kernel leg")
+    h = headline_leg(torch, pool, layout, sources, dests, steps, warmup, label=f"tp{tp} rank")
+    step_s = h["elapsed"] / steps
+    link_gbs = h["link_bytes_per_step"] / step_s / 1e9
+    kernels = {}
+    for name in ("save", "restore"):
+        gbs = k["hbm_bytes"] / (k[f"{name}_ms"] / 1000) / 1e9
+        kernels[name] = {"ms": round(k[f"{name}_ms"], 4), "hbm_gbs": round(gbs, 1),
+                         "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    del pool
+    return {"tp": tp, "pool": list(shape.shape), "blocks_saved": blocks, "blocks_restored": blocks,
+            "block_bytes_bf16": shape.block_bytes_bf16, "entry_bytes": k["logical_entry"],
+            "kernels": dict(kernels, algorithmic_bytes_per_launch=k["hbm_bytes"]),
+            "pinned_step": {"ms": round(1000 * step_s, 4),
+                            "logical_kv_gbs": round(2 * blocks * shape.block_bytes_bf16 / step_s / 1e9, 2),
+                            "link_gbs": round(link_gbs, 2), "link_frac_of_spec": round(link_gbs / (2 * PCIE_PEAK_GBS), 4),
+                            "streams_concurrent": h["streams_concurrent"]}}
 
 
 def profiler_tool_loaded(maps_path="/proc/self/maps"):
@@ -1708,6 +1747,10 @@ def main():
         },
         "inventory": inventory,
     }
+    if not args.skip_tp_rank:
+        log("config 2 at one TP=8 rank's share of the pool")
+        result["tp8_rank_shape"] = tp_rank_leg(torch, ops, scale_dtype, args.steps, args.warmup)
+        log(f"tp8 rank: {json.dumps(result['tp8_rank_shape'])}")
     if not args.skip_store:
         log("store_kvcache leg")
         result["store_kvcache"] = store_leg(torch, ops, pool, concurrency=not args.skip_store_concurrency)

@@ -120,7 +120,9 @@ def make_pool(device, layers=4, blocks=12, bs=256, heads=8, hd=128, seed=0):
 
 # The vector kernels cover head_dim 64, 128 and 256 in tiles of 4-16 rows; the
 # last three geometries leave a ragged last tile in every plane (15, 7 and 6 rows).
+# heads=1, hd=128 is one tensor-parallel rank's share of Qwen3-8B at TP=8.
 @pytest.mark.parametrize("geometry", [dict(), dict(layers=2, blocks=6, bs=256, heads=1, hd=4),
+                                      dict(layers=3, blocks=6, bs=256, heads=1, hd=128),
                                       dict(layers=3, blocks=7, bs=32, heads=3, hd=96),
                                       dict(layers=2, blocks=6, bs=5, heads=3, hd=128),
                                       dict(layers=1, blocks=6, bs=7, heads=1, hd=64),
