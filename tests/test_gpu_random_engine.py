@@ -136,7 +136,8 @@ def test_random_request_streams_keep_every_block_intact(gpu, fp8, split, batched
 
 
 @pytest.mark.parametrize("heads,head_dim,scale_dtype", [(4, 64, torch.float32), (1, 96, torch.float32),
-                                                        (2, 128, torch.bfloat16), (1, 256, torch.bfloat16)])
+                                                        (2, 128, torch.bfloat16), (1, 256, torch.bfloat16),
+                                                        (1, 128, torch.float32)])  # last: a TP=8 rank of Qwen3-8B
 @pytest.mark.parametrize("fp8", [True, False], ids=["fp8", "bf16"])
 def test_random_request_streams_on_other_head_shapes_and_scales(gpu, heads, head_dim, scale_dtype, fp8, monkeypatch):
     # head_dim 96 takes the generic kernels (one thread per row) and staged restores only.
